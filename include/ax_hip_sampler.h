@@ -1,0 +1,234 @@
+/*
+ * ax_hip_sampler.h — C ABI of the MI355X (gfx950) per-step token sampler.
+ *
+ * This is the boundary a `hip-sys` crate binds, as a sibling of the
+ * reference's `crates/mlx-sys` (plain C header, opaque context handle,
+ * `int` status codes, thread-local last-error string:
+ * crates/mlx-sys/native/ax_shim.h:24-40,106-110 and
+ * crates/mlx-sys/native/ax_shim.cpp:47-57 in the reference).
+ *
+ * Conventions
+ *   - Every entry point returns AXS_OK (0) or a nonzero AXS_E_* code; the
+ *     message of the last failure on the calling thread is returned by
+ *     axs_last_error().  A caller that gets a nonzero status falls back to
+ *     its CPU sampler, as the reference's GPU helpers decline with `None`
+ *     (crates/ax-engine-mlx/src/generate.rs:221-238).
+ *   - Every array pointer in the *_desc / *_outputs structs is a DEVICE
+ *     pointer (HBM), borrowed for the duration of the call.  Outputs are
+ *     caller-allocated.  `stream` is a hipStream_t passed as void* (NULL =
+ *     the null stream); all work is enqueued on it and the call returns
+ *     without synchronising.
+ *   - No torch or HIP types appear in the signatures.
+ *   - Calls that share one context must not overlap (the context owns the
+ *     device workspace); use one context per thread or serialise.
+ */
+#ifndef AX_HIP_SAMPLER_H
+#define AX_HIP_SAMPLER_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define AXS_ABI_VERSION 1
+
+/* status codes */
+#define AXS_OK            0
+#define AXS_E_INVALID     1   /* bad argument (shape, pointer, size) */
+#define AXS_E_HIP         2   /* HIP runtime error */
+#define AXS_E_CAPACITY    3   /* larger than the context was created for */
+#define AXS_E_UNSUPPORTED 4
+
+/* logits element types; bf16 is widened exactly to f32 before any arithmetic,
+ * as production casts the lm_head output to f32 before sampling
+ * (crates/ax-engine-mlx/src/model/mod.rs:1771-1774). */
+#define AXS_DTYPE_F32  0
+#define AXS_DTYPE_BF16 1
+
+#define AXS_NONE_U32 0xFFFFFFFFu
+
+/*
+ * Per-row sampling parameters.  Mirrors MlxSamplingParams
+ * (crates/ax-engine-mlx/src/sampling.rs:39-114) and the core SamplingParams
+ * (crates/ax-engine-core/src/sampling.rs:7-41); the activity predicates are
+ * the reference's:
+ *   repetition penalty active iff finite, > 0 and != 1      (sampling.rs:91-95)
+ *   min-p active iff has_min_p and min_p finite and > 0     (sampling.rs:86-89)
+ *   no-repeat n-gram active iff no_repeat_ngram_size > 0    (sampling.rs:107-109)
+ * presence_penalty, frequency_penalty, and the logit bias / allowed-token mask
+ * of axs_batch_desc do not exist in the reference (its OpenAI route rejects
+ * them: crates/ax-engine-server/src/openai/requests.rs:1240-1281); their
+ * semantics here are build-defined (OpenAI convention):
+ *   for each id t < V with count c > 0 in the repetition window:
+ *       l = l - frequency_penalty * (float)c;  l = l - presence_penalty;
+ *   then l += bias (each listed entry, in list order), then masked ids -> -inf.
+ * Processor order: repetition -> presence/frequency -> bias -> mask -> n-gram
+ * ban -> temperature.  Sizeof = 64 bytes.
+ */
+typedef struct axs_sampling_params {
+    float    temperature;             /* <= 0: greedy argmax                  */
+    float    top_p;                   /* >= 1: no nucleus truncation          */
+    uint32_t top_k;                   /* 0: no top-k truncation               */
+    float    min_p;                   /* read only when has_min_p != 0        */
+    uint32_t has_min_p;               /* Option<f32> discriminant             */
+    float    repetition_penalty;      /* 1.0: off                             */
+    uint32_t repetition_context_size; /* AXS_NONE_U32: whole history          */
+    uint32_t no_repeat_ngram_size;    /* 0: off                               */
+    uint32_t ngram_window;            /* reference default 128                */
+    float    presence_penalty;        /* build extension, 0: off              */
+    float    frequency_penalty;       /* build extension, 0: off              */
+    uint32_t reserved0;
+    uint64_t seed;                    /* Philox key when no uniforms supplied */
+    uint64_t step;                    /* Philox counter (decode step)         */
+} axs_sampling_params;
+
+/*
+ * One batched sampling step.  Replaces, for a [B, V] logits tensor already in
+ * HBM, the host readback + serial per-row loop of sample_batched_host
+ * (crates/ax-engine-mlx/src/batched_sampling.rs:123-149) and
+ * resolve_batched_group_tokens (crates/ax-engine-mlx/src/runner/mod.rs:3132-3210),
+ * each row following sample_categorical_into
+ * (crates/ax-engine-mlx/src/sampling.rs:204-316).
+ */
+typedef struct axs_batch_desc {
+    const void*     logits;          /* [batch, row_stride] of dtype            */
+    int32_t         dtype;           /* AXS_DTYPE_*                             */
+    int32_t         batch;
+    int32_t         vocab;
+    int32_t         reserved0;
+    int64_t         row_stride;      /* elements between rows (>= vocab)        */
+    const axs_sampling_params* params;   /* [batch]                             */
+    /* Token history (prompt + generated tail, oldest first) in CSR form, the
+     * `repetition_tokens` slice of sample_categorical_into.  NULL = none. */
+    const uint32_t* history;         /* [history_len]                           */
+    const int64_t*  history_offsets; /* [batch + 1]                             */
+    int64_t         history_len;
+    /* Allowed-token bitmask (build extension): bit (t & 31) of word t >> 5,
+     * LSB = lowest id; 0 = disallowed.  NULL = all allowed. */
+    const uint32_t* mask_words;      /* [batch, mask_stride]                    */
+    int64_t         mask_stride;     /* u32 words per row, >= ceil(vocab / 32)  */
+    /* Sparse logit bias (build extension) in CSR form.  NULL = none. */
+    const uint32_t* bias_ids;        /* [bias_len]                              */
+    const float*    bias_values;     /* [bias_len], finite                      */
+    const int64_t*  bias_offsets;    /* [batch + 1]                             */
+    int64_t         bias_len;
+    /* Supplied uniforms in [0, 1], one per row, consumed only when the row
+     * draws.  NULL = Philox4x32-10 with key = params.seed, counter =
+     * (row, step_lo, step_hi, 0), uniform = (word0 >> 8) * 2^-24. */
+    const float*    uniforms;        /* [batch]                                 */
+} axs_batch_desc;
+
+/* per-row flag bits written to axs_outputs.flags */
+#define AXS_FLAG_GREEDY          (1u << 0)  /* temperature <= 0: argmax          */
+#define AXS_FLAG_ARGMAX_FALLBACK (1u << 1)  /* zero / non-finite mass or empty
+                                               min-p set: argmax (sampling.rs:265,281,292,299) */
+#define AXS_FLAG_DREW            (1u << 2)  /* a uniform was consumed            */
+#define AXS_FLAG_EXACT_PATH      (1u << 3)  /* row resolved by the exact
+                                               ordered-sum path (second pass)     */
+#define AXS_FLAG_NEAR_DRAW       (1u << 4)  /* |cum - u*F| < 1e-6 F at the draw  */
+#define AXS_FLAG_NEAR_NUCLEUS    (1u << 5)  /* |cum - top_p*total| < 1e-6 total  */
+#define AXS_FLAG_NEAR_MINP       (1u << 6)  /* |p - min_p| < 1e-6 min_p          */
+#define AXS_FLAG_NEAR_TIE        (1u << 7)  /* p within 2 ulp across the top-k cut */
+#define AXS_FLAG_ERROR           (1u << 31) /* invalid row input (token 0)       */
+
+typedef struct axs_outputs {
+    uint32_t* token_ids;   /* [batch], required                                   */
+    float*    logprobs;    /* [batch] or NULL: greedy rows -ln sum exp(l - max)
+                              (crates/ax-engine-core/src/sampling.rs:177-190);
+                              sampled rows max(ln(p/F), -30)
+                              (crates/ax-engine-mlx/src/sampling.rs:156-160)      */
+    uint32_t* flags;       /* [batch] or NULL, AXS_FLAG_* bits                    */
+    uint32_t* kept_ids;    /* [batch, kept_cap] or NULL: the kept set in draw order
+                              (diagnostics, e.g. top-k set parity)                */
+    uint32_t* kept_count;  /* [batch] or NULL: size of the kept set               */
+    int32_t   kept_cap;
+    int32_t   reserved0;
+} axs_outputs;
+
+/*
+ * MTP speculative verify for `batch` sequences of draft depth `depth` (<= 7):
+ * target logits [batch, depth + 1, row_stride], draft logits
+ * [batch, depth, row_stride].  Per sequence and position i the law is the
+ * reference's function-level one:
+ *   P_i = token_distribution(target_i), Q_i = token_distribution(draft_i)
+ *        (crates/ax-engine-mlx/src/sampling.rs:647-707)
+ *   ln q = max(ln(max(Q_i(d_i), 1e-37)), -30)        (sampling.rs:156-160)
+ *   accept iff u_i < min(1, P_i(d_i) / max(exp(ln q'), 1e-37)), with
+ *   ln q' = ln q * (T_d / T_t) when both > 0 and differ by > 1e-6
+ *        (crates/ax-engine-mlx/src/runner/mod.rs:12388-12419)
+ *   on reject: residual max(P_i - Q_i, 0) in ascending id order
+ *        (sampling.rs:733-752) drawn with the tail uniform;
+ *   all accepted: bonus = sample_categorical_into(target_depth) with the tail
+ *        uniform (crates/ax-engine-mlx/src/runner/mod.rs:9732-9775).
+ * Uniforms: [batch, depth + 1]; slot i < depth is position i's accept uniform,
+ * slot depth the residual/bonus uniform.  NULL = Philox counter
+ * (row, step_lo, step_hi, 1), words 0..3 then (row, step_lo, step_hi, 2) ...
+ */
+typedef struct axs_mtp_desc {
+    const void*     target_logits;   /* [batch, depth + 1, row_stride]          */
+    const void*     draft_logits;    /* [batch, depth, row_stride]              */
+    int32_t         dtype;
+    int32_t         batch;
+    int32_t         depth;
+    int32_t         vocab;
+    int64_t         row_stride;
+    const uint32_t* draft_ids;       /* [batch, depth]                          */
+    const axs_sampling_params* target_params; /* [batch]                        */
+    const axs_sampling_params* draft_params;  /* [batch]                        */
+    const float*    uniforms;        /* [batch, depth + 1] or NULL              */
+} axs_mtp_desc;
+
+#define AXS_MTP_FLAG_RESIDUAL    (1u << 0)  /* tail token came from the residual */
+#define AXS_MTP_FLAG_BONUS       (1u << 1)  /* all drafts accepted, bonus drawn  */
+#define AXS_MTP_FLAG_NEAR_ACCEPT (1u << 2)  /* |u - p/q| < 1e-6 at a decision   */
+#define AXS_MTP_FLAG_NEAR        (1u << 3)  /* a distribution had a near flag   */
+#define AXS_MTP_FLAG_ERROR       (1u << 31)
+
+typedef struct axs_mtp_outputs {
+    uint32_t* out_ids;       /* [batch, depth + 1]: accepted prefix then tail   */
+    uint32_t* out_count;     /* [batch]: accept_count + 1                        */
+    uint32_t* accept_count;  /* [batch] or NULL                                  */
+    uint32_t* flags;         /* [batch] or NULL                                  */
+} axs_mtp_outputs;
+
+typedef struct axs_context axs_context;
+
+/* ABI version of the loaded library (AXS_ABI_VERSION). */
+int axs_abi_version(void);
+
+/* Thread-local message of the last failed call on this thread ("" if none). */
+const char* axs_last_error(void);
+
+/* Creates a sampler context on `device` with device workspace sized for up to
+ * max_batch rows of up to max_vocab entries (MTP counts depth*2+1 rows per
+ * sequence).  Replaces the reference's per-request sampler buffers
+ * (probs_buf / logits_buf / candidates_buf of sample_categorical_into,
+ * crates/ax-engine-mlx/src/sampling.rs:204-212). */
+int axs_context_create(int device, int max_batch, int max_vocab, axs_context** out);
+int axs_context_destroy(axs_context* ctx);
+
+/* Batched sampling step (see axs_batch_desc). */
+int axs_sample_batch(axs_context* ctx, const axs_batch_desc* desc,
+                     const axs_outputs* out, void* stream);
+
+/* Greedy batched argmax + logprob over [batch, row_stride] logits: first
+ * maximum (lowest id) wins, NaN skipped, all-NaN row -> 0
+ * (crates/ax-engine-mlx/src/sampling.rs:954-966); replaces argmax_batched
+ * (crates/ax-engine-mlx/src/batched_sampling.rs:102-111) and the Metal
+ * sample_argmax_logprob_batched_f32 kernel
+ * (metal/kernels/phase1_dense_path.metal:1273-1341).  out_logprob may be NULL;
+ * it receives -ln sum_{finite l} exp(l - max) (NaN when the max is not finite). */
+int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
+                     int vocab, int64_t row_stride, uint32_t* out_ids,
+                     float* out_logprob, void* stream);
+
+/* MTP speculative verify (see axs_mtp_desc). */
+int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
+                   const axs_mtp_outputs* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* AX_HIP_SAMPLER_H */
