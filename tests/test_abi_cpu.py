@@ -1,0 +1,70 @@
+"""CPU-side checks of the C ABI: the built library loads and exports every
+entry point include/ax_hip_sampler.h declares (no GPU call is made)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def header_functions():
+    with open(os.path.join(ROOT, "include", "ax_hip_sampler.h")) as f:
+        src = f.read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"\b(axs_[a-z_]+)\s*\(", src)))
+
+
+def test_header_declares_the_entry_points():
+    fns = header_functions()
+    for f in ("axs_context_create", "axs_context_destroy", "axs_sample_batch",
+              "axs_argmax_batch", "axs_mtp_verify", "axs_last_error", "axs_abi_version"):
+        assert f in fns
+
+
+def test_library_exports_every_declared_symbol():
+    from ax_sampler import _abi
+
+    assert os.path.exists(_abi.LIB_PATH), "build first: __graft_entry__.build()"
+    out = subprocess.run(["nm", "-D", "--defined-only", _abi.LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (axs_[a-z_]+)\b", out))
+    missing = [f for f in header_functions() if f not in exported]
+    assert not missing, missing
+    assert set(_abi.EXPORTS) <= exported
+
+
+def test_library_loads_without_touching_the_gpu():
+    from ax_sampler import _abi
+
+    L = ctypes.CDLL(_abi.LIB_PATH)
+    L.axs_abi_version.restype = ctypes.c_int
+    assert L.axs_abi_version() == 1
+    L.axs_last_error.restype = ctypes.c_char_p
+    assert L.axs_last_error() == b""
+
+
+def test_struct_layouts_match_the_header():
+    from ax_sampler import _abi
+    from ax_sampler.params import PARAMS_DTYPE
+
+    assert PARAMS_DTYPE.itemsize == 64
+    assert ctypes.sizeof(_abi.BatchDesc) == 120
+    assert ctypes.sizeof(_abi.Outputs) == 48
+    assert ctypes.sizeof(_abi.MtpDesc) == 72
+    assert ctypes.sizeof(_abi.MtpOutputs) == 32
+
+
+def test_c_struct_sizes_from_the_compiler(tmp_path):
+    src = tmp_path / "s.c"
+    src.write_text(
+        '#include "ax_hip_sampler.h"\n#include <stdio.h>\n#include <stddef.h>\n'
+        "int main(){printf(\"%zu %zu %zu %zu %zu\\n\", sizeof(axs_sampling_params),"
+        " sizeof(axs_batch_desc), sizeof(axs_outputs), sizeof(axs_mtp_desc),"
+        " sizeof(axs_mtp_outputs));return 0;}\n")
+    exe = tmp_path / "s"
+    subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
+    sizes = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
+    assert sizes == ["64", "120", "48", "72", "32"]
