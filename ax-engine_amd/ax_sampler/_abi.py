@@ -56,7 +56,12 @@ EXPORTS = (
     "axs_sample_batch",
     "axs_argmax_batch",
     "axs_mtp_verify",
+    "axs_timing_enable",
+    "axs_timing_read",
 )
+
+KERNEL_CHUNK, KERNEL_FINISH, KERNEL_EXACT_MAT, KERNEL_EXACT_ROW, KERNEL_MTP = range(5)
+KERNEL_NAMES = ("k_chunk", "k_finish", "k_exact_mat", "k_exact_row", "k_mtp_verify")
 
 
 def build_library(verbose: bool = False) -> str:
@@ -169,6 +174,10 @@ def lib():
             L.axs_argmax_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_mtp_verify.restype = i32
             L.axs_mtp_verify.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOutputs), vp]
+            L.axs_timing_enable.restype = i32
+            L.axs_timing_enable.argtypes = [vp, i32]
+            L.axs_timing_read.restype = i32
+            L.axs_timing_read.argtypes = [vp, i32, C.POINTER(C.c_double), C.POINTER(C.c_int)]
             if L.axs_abi_version() != 1:
                 raise SamplerError("ABI version mismatch")
             _lib = L

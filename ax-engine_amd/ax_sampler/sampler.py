@@ -140,6 +140,16 @@ class HipSampler:
         except Exception:
             pass
 
+    def timing(self, enable: bool) -> None:
+        """Brackets every launch with hipEvents on its stream (clears records)."""
+        _abi.check(self.L.axs_timing_enable(self.ctx, 1 if enable else 0))
+
+    def timing_read(self, kernel: int):
+        """(total ms, launches) of one kernel class since timing was enabled."""
+        ms, n = C.c_double(), C.c_int()
+        _abi.check(self.L.axs_timing_read(self.ctx, kernel, C.byref(ms), C.byref(n)))
+        return ms.value, n.value
+
     def _stream(self, stream):
         torch = _torch()
         s = torch.cuda.current_stream(self.device) if stream is None else stream

@@ -86,16 +86,24 @@ class Workload:
 
 
 def _zipf_head(rng: np.random.Generator, B: int, V: int, s: float = 1.1):
-    """-s ln(rank) over a per-row random permutation; also returns the ids of
-    the 64 highest ranks per row."""
-    ranks = np.empty((B, V), dtype=np.float32)
-    top = np.empty((B, 64), dtype=np.uint32)
-    base = np.arange(1, V + 1, dtype=np.float32)
+    """-s ln(rank) over a per-row random permutation of the ids; also returns
+    the ids of the 64 highest ranks per row.  The permutation of row r is the
+    affine bijection id -> (a_r * id + b_r) mod V with a_r coprime to V."""
+    a = rng.integers(1, V, size=B, dtype=np.int64)
     for r in range(B):
-        perm = rng.permutation(V)
-        ranks[r, perm] = base
-        top[r] = perm[:64]
-    return (-s * np.log(ranks)).astype(np.float32), top
+        while np.gcd(int(a[r]), V) != 1:
+            a[r] = (a[r] + 1) % V or 1
+    b = rng.integers(0, V, size=B, dtype=np.int64)
+    ids = np.arange(V, dtype=np.int64)
+    rank0 = (a[:, None] * ids[None, :] + b[:, None]) % V  # 0-based rank of each id
+    head = (-s * np.log((rank0 + 1).astype(np.float32))).astype(np.float32)
+    # ids of ranks 0..63: invert the affine map with a_r^-1 mod V
+    top = np.empty((B, 64), dtype=np.uint32)
+    ks = np.arange(64, dtype=np.int64)
+    for r in range(B):
+        ainv = pow(int(a[r]), -1, V)
+        top[r] = ((ks - b[r]) % V * ainv % V).astype(np.uint32)
+    return head, top
 
 
 def _histories(rng, B, V, H, hot):

@@ -33,6 +33,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cstdlib>
 #include <mutex>
 #include <new>
 #include <string>
@@ -46,7 +47,8 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NT_CHUNK = 256;
-constexpr uint32_t CH_MAX = 8192;     // ids per chunk (upper bound)
+constexpr uint32_t SEG_MAX = 32768;   // ids per segment (upper bound)
+constexpr uint32_t MAX_SEGS = 1024;   // segments per row (upper bound)
 constexpr uint32_t CAPC = 512;        // candidates kept per chunk
 constexpr int NT_FIN = 256;
 constexpr uint32_t FIN_CAP = 2048;    // candidates merged per row in k_finish
@@ -106,6 +108,7 @@ struct KArgs {
     int32_t mtp_depth;    // > 0: MTP layout
     int32_t mtp_batch;
     int32_t want_logprob;
+    int32_t vec;          // rows are 16-byte aligned: vector loads
     int64_t stride;
     const axs_sampling_params* params;
     const axs_sampling_params* params2;
@@ -199,16 +202,26 @@ __device__ __forceinline__ float row_uniform(const KArgs& a, int r, const axs_sa
 }
 
 // --------------------------------------------------------------------------
-// logits processors (chunk-local LDS tables)
+// logits processors: per-segment LDS tables
+//   spec  bit per id of the segment: the id has a history count or a bias entry
+//   ban   bit per id: banned by the no-repeat n-gram rule
+//   hash  open-addressing table offset → occurrence count in the repetition
+//         window (only ids that occur); if it ever fills, counts are taken by
+//         scanning the window in HBM for the (few) flagged ids
 // --------------------------------------------------------------------------
+constexpr uint32_t HSLOTS = 2048;
+constexpr uint32_t HBITS = 11;
+
 struct ProcLds {
-    uint32_t cnt[CH_MAX / 2];      // u16 occurrence counts in the repetition window
-    uint32_t spec[CH_MAX / 32];    // ids carrying a bias entry
-    uint32_t ban[CH_MAX / 32];     // ids banned by the no-repeat n-gram rule
+    uint32_t spec[SEG_MAX / 32];
+    uint32_t ban[SEG_MAX / 32];
+    uint32_t hkey[HSLOTS];   // offset + 1, 0 = empty
+    uint32_t hval[HSLOTS];   // occurrence count
     uint32_t bias_id[BIAS_LDS];
     float bias_v[BIAS_LDS];
     uint32_t nbias;
-    uint32_t err;
+    uint32_t err;    // bias entries beyond BIAS_LDS in one segment
+    uint32_t hfull;  // the hash filled up
 };
 
 struct RowCtx {
@@ -247,7 +260,6 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int r) {
     c.rep_on = ref_proc && uses_rep(c.p) && keep > 0;
     c.pf_on = (c.p.presence_penalty != 0.0f || c.p.frequency_penalty != 0.0f) && keep > 0;
     c.cnt_on = c.rep_on || c.pf_on;
-    if (c.cnt_on && keep > 65535) c.err = true;  // u16 counts
     c.ban_on = ref_proc && c.p.no_repeat_ngram_size > 0 && nhist >= (int64_t)c.p.no_repeat_ngram_size;
     c.bias_on = false;
     if (a.bias_ids && a.bias_off && a.mtp_depth == 0) {
@@ -268,20 +280,44 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int r) {
     return c;
 }
 
-// Builds the chunk's LDS tables for ids in [lo, hi).  Block-uniform control.
-__device__ void proc_setup(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi, ProcLds& L) {
+__device__ __forceinline__ uint32_t hslot(uint32_t off) { return (off * 2654435761u) >> (32 - HBITS); }
+
+__device__ __forceinline__ void hash_add(ProcLds& L, uint32_t off) {
+    const uint32_t key = off + 1u;
+    uint32_t h = hslot(off);
+    for (uint32_t probe = 0; probe < HSLOTS; ++probe) {
+        uint32_t k = L.hkey[h];
+        if (k == 0u) {
+            uint32_t prev = atomicCAS(&L.hkey[h], 0u, key);
+            k = prev == 0u ? key : prev;
+        }
+        if (k == key) {
+            atomicAdd(&L.hval[h], 1u);
+            return;
+        }
+        h = (h + 1u) & (HSLOTS - 1u);
+    }
+    L.hfull = 1u;
+}
+
+// Builds the segment's LDS tables for ids in [lo, hi).  Block-uniform control.
+__device__ __forceinline__ void proc_setup(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi,
+                                           ProcLds& L) {
     const int tid = threadIdx.x;
-    uint32_t n = hi - lo;
+    const uint32_t nw = (hi - lo + 31u) / 32u;
     if (tid == 0) {
         L.nbias = 0;
         L.err = 0;
+        L.hfull = 0;
+    }
+    for (uint32_t i = tid; i < nw; i += NT_CHUNK) {
+        L.spec[i] = 0u;
+        L.ban[i] = 0u;
     }
     if (c.cnt_on)
-        for (uint32_t i = tid; i < (n + 1) / 2; i += NT_CHUNK) L.cnt[i] = 0;
-    if (c.bias_on || c.ban_on)
-        for (uint32_t i = tid; i < (n + 31) / 32; i += NT_CHUNK) {
-            L.spec[i] = 0;
-            L.ban[i] = 0;
+        for (uint32_t i = tid; i < HSLOTS; i += NT_CHUNK) {
+            L.hkey[i] = 0u;
+            L.hval[i] = 0u;
         }
     __syncthreads();
     if (c.cnt_on) {
@@ -289,7 +325,8 @@ __device__ void proc_setup(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_
             uint32_t t = a.hist[i];
             if (t >= lo && t < hi) {
                 uint32_t off = t - lo;
-                atomicAdd(&L.cnt[off >> 1], 1u << ((off & 1u) * 16u));
+                hash_add(L, off);
+                atomicOr(&L.spec[off >> 5], 1u << (off & 31u));
             }
         }
     }
@@ -348,116 +385,197 @@ __device__ void proc_setup(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_
     __syncthreads();
 }
 
-// Applies the processors to logit l of id e (repetition → presence/frequency
-// → bias → mask → n-gram ban), exactly as the oracle orders them.
-__device__ __forceinline__ float proc_apply(const KArgs& a, const RowCtx& c, const ProcLds& L,
-                                            int r, uint32_t lo, uint32_t e, float l) {
-    uint32_t off = e - lo;
-    if (c.cnt_on) {
-        uint32_t cnt = (L.cnt[off >> 1] >> ((off & 1u) * 16u)) & 0xFFFFu;
-        if (cnt) {
-            if (c.rep_on) {
-                float rp = c.p.repetition_penalty;
-                l = l < 0.0f ? __fmul_rn(l, rp) : __fdiv_rn(l, rp);
+// Processor flags of a row
+constexpr uint32_t PF_REP = 1u, PF_PF = 2u, PF_CNT = 4u, PF_BIAS = 8u;
+
+// Repetition → presence/frequency → bias for one id that carries a history
+// count or a bias entry (mask and n-gram ban are applied by the caller).
+__device__ __forceinline__ float proc_special(const uint32_t* __restrict__ hist, const ProcLds& L,
+                                              uint32_t off, uint32_t e, float l, uint32_t pfl,
+                                              float rep, float freq, float pres, int64_t w0,
+                                              int64_t w1) {
+    if (pfl & PF_CNT) {
+        // occurrences of e in the repetition window, from the LDS hash
+        const uint32_t key = off + 1u;
+        uint32_t h = hslot(off);
+        uint32_t cnt = 0;
+        bool found = false;
+        for (uint32_t probe = 0; probe < HSLOTS; ++probe) {
+            uint32_t k = L.hkey[h];
+            if (k == key) {
+                cnt = L.hval[h];
+                found = true;
+                break;
             }
-            if (c.pf_on) {
-                l = __fsub_rn(l, __fmul_rn(c.p.frequency_penalty, (float)cnt));
-                l = __fsub_rn(l, c.p.presence_penalty);
+            if (k == 0u) break;
+            h = (h + 1u) & (HSLOTS - 1u);
+        }
+        if (!found && L.hfull) {  // the table overflowed: count in HBM
+            for (int64_t i = w0; i < w1; ++i) cnt += hist[i] == e ? 1u : 0u;
+        }
+        if (cnt) {
+            if (pfl & PF_REP) l = l < 0.0f ? __fmul_rn(l, rep) : __fdiv_rn(l, rep);
+            if (pfl & PF_PF) {
+                l = __fsub_rn(l, __fmul_rn(freq, (float)cnt));
+                l = __fsub_rn(l, pres);
             }
         }
     }
-    if (c.bias_on && ((L.spec[off >> 5] >> (off & 31u)) & 1u)) {
+    if (pfl & PF_BIAS)
         for (uint32_t j = 0; j < L.nbias; ++j)
             if (L.bias_id[j] == e) l = __fadd_rn(l, L.bias_v[j]);
-    }
-    if (c.mask_on) {
-        uint32_t w = a.mask[(size_t)r * a.mask_stride + (e >> 5)];
-        if (!((w >> (e & 31u)) & 1u)) l = -INFINITY;
-    }
-    if (c.ban_on && ((L.ban[off >> 5] >> (off & 31u)) & 1u)) l = -INFINITY;
     return l;
 }
 
-// Loads the chunk [lo, hi) of row r into registers (ids lo + (j*256+t)*EPV + q)
-// and applies the processors; ids >= hi read as NaN (never a max, never a
-// candidate).
-template <int DT, int NV, bool VEC>
-__device__ __forceinline__ void load_chunk(const KArgs& a, const RowCtx& c, const ProcLds& L,
-                                           int r, uint32_t lo, uint32_t hi,
-                                           float (&v)[NV * (DT == AXS_DTYPE_BF16 ? 8 : 4)]) {
-    constexpr int EPV = DT == AXS_DTYPE_BF16 ? 8 : 4;
+// Segment geometry: thread t holds NV vectors of EPV consecutive ids; vector j
+// covers ids lo + (j*256 + t)*EPV + [0, EPV).
+template <int DT>
+struct Ev {
+    static constexpr int EPV = DT == AXS_DTYPE_BF16 ? 8 : 4;
+};
+
+template <int DT, int NV>
+struct Seg {
+    static constexpr int EPV = Ev<DT>::EPV;
+    u32x4 raw[NV];     // the logits as loaded (bf16 pairs or f32 bits)
+    uint32_t mw[NV];   // mask word of each vector (when masked)
+};
+
+// Issues every load of the segment (16-byte nontemporal vectors when the rows
+// are 16-byte aligned; element loads at the tail or otherwise).  ids >= hi read
+// as NaN: never a maximum, never a candidate.
+template <int DT, int NV>
+__device__ __forceinline__ void seg_load(const KArgs& a, int r, uint32_t lo, uint32_t hi,
+                                         bool vec, bool masked, Seg<DT, NV>& S) {
+    constexpr int EPV = Ev<DT>::EPV;
     const int tid = threadIdx.x;
     const char* rp = row_ptr(a, r);
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         uint32_t e0 = lo + ((uint32_t)j * NT_CHUNK + tid) * EPV;
-        if (VEC && e0 + EPV <= hi) {
+        if (vec && e0 + EPV <= hi) {
+            S.raw[j] = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)e0 * (EPV == 8 ? 2 : 4)));
+        } else {
+            uint32_t w[4];
             if (DT == AXS_DTYPE_BF16) {
-                u32x4 w = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)e0 * 2));
-                uint32_t ws[4] = {w[0], w[1], w[2], w[3]};
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
-                    v[j * EPV + 2 * q] = __uint_as_float(ws[q] << 16);
-                    v[j * EPV + 2 * q + 1] = __uint_as_float(ws[q] & 0xFFFF0000u);
+                    uint32_t ea = e0 + 2 * q, eb = ea + 1;
+                    uint32_t lo16 = ea < hi ? ((const uint16_t*)rp)[ea] : 0x7FC0u;
+                    uint32_t hi16 = eb < hi ? ((const uint16_t*)rp)[eb] : 0x7FC0u;
+                    w[q] = lo16 | (hi16 << 16);
                 }
             } else {
-                f32x4 w = __builtin_nontemporal_load((const f32x4*)(rp + (size_t)e0 * 4));
-                v[j * EPV + 0] = w[0];
-                v[j * EPV + 1] = w[1];
-                v[j * EPV + 2] = w[2];
-                v[j * EPV + 3] = w[3];
-            }
-        } else {
 #pragma unroll
-            for (int q = 0; q < EPV; ++q) {
-                uint32_t e = e0 + q;
-                float x = NAN;
-                if (e < hi) {
-                    if (DT == AXS_DTYPE_BF16)
-                        x = __uint_as_float((uint32_t)((const uint16_t*)rp)[e] << 16);
-                    else
-                        x = ((const float*)rp)[e];
+                for (int q = 0; q < 4; ++q) {
+                    uint32_t ea = e0 + q;
+                    w[q] = ea < hi ? ((const uint32_t*)rp)[ea] : 0x7FC00000u;
                 }
-                v[j * EPV + q] = x;
             }
+            S.raw[j] = u32x4{w[0], w[1], w[2], w[3]};
         }
-    }
-    if (c.any_proc) {
-#pragma unroll
-        for (int j = 0; j < NV; ++j) {
-            uint32_t e0 = lo + ((uint32_t)j * NT_CHUNK + tid) * EPV;
-#pragma unroll
-            for (int q = 0; q < EPV; ++q) {
-                uint32_t e = e0 + q;
-                if (e < hi) v[j * EPV + q] = proc_apply(a, c, L, r, lo, e, v[j * EPV + q]);
-            }
-        }
+        S.mw[j] = (masked && e0 < hi) ? a.mask[(size_t)r * a.mask_stride + (e0 >> 5)] : 0xFFFFFFFFu;
     }
 }
 
-template <int DT, int NV>
-__device__ __forceinline__ uint32_t elem_id(uint32_t lo, int k) {
-    constexpr int EPV = DT == AXS_DTYPE_BF16 ? 8 : 4;
-    int j = k / EPV, q = k % EPV;
-    return lo + ((uint32_t)j * NT_CHUNK + threadIdx.x) * EPV + q;
+template <int DT>
+__device__ __forceinline__ float unpack(const u32x4& w, int q) {
+    if (DT == AXS_DTYPE_BF16) {
+        uint32_t x = w[q >> 1];
+        return __uint_as_float((q & 1) ? (x & 0xFFFF0000u) : (x << 16));
+    }
+    return __uint_as_float(w[q]);
+}
+
+// Visits every id of the segment once, with its processed logit: f(id, l).
+// Ids without a special bit come from the thread's registers (mask applied
+// inline); ids with a history count, a bias entry or an n-gram ban are
+// visited in a second loop over the segment's bitmaps, which re-reads their
+// raw logits (a few per segment) and applies every processor in order.
+template <int DT, int NV, typename F>
+__device__ __forceinline__ void seg_visit(const KArgs& a, const RowCtx& c, const ProcLds& L, int r,
+                                          uint32_t lo, uint32_t hi, Seg<DT, NV>& S, F&& f) {
+    constexpr int EPV = Ev<DT>::EPV;
+    const int tid = threadIdx.x;
+    const uint32_t pfl = (c.rep_on ? PF_REP : 0u) | (c.pf_on ? PF_PF : 0u) |
+                         (c.cnt_on ? PF_CNT : 0u) | (c.bias_on ? PF_BIAS : 0u);
+    const bool special = pfl != 0u || c.ban_on;
+#pragma unroll
+    for (int j = 0; j < NV; ++j) {
+        // recompute from the raw registers in every pass (keeps the unpacked
+        // values out of the register budget)
+        asm volatile("" : "+v"(S.raw[j]));
+        const uint32_t e0 = lo + ((uint32_t)j * NT_CHUNK + tid) * EPV;
+        const uint32_t off0 = e0 - lo;
+        uint32_t skip = 0;
+        if (special)
+            skip = ((L.spec[off0 >> 5] | L.ban[off0 >> 5]) >> (off0 & 31u)) & ((1u << EPV) - 1u);
+#pragma unroll
+        for (int q = 0; q < EPV; ++q) {
+            if ((skip >> q) & 1u) continue;
+            float l = unpack<DT>(S.raw[j], q);
+            if (c.mask_on && !((S.mw[j] >> ((e0 + q) & 31u)) & 1u)) l = -INFINITY;
+            f(e0 + q, l);
+        }
+    }
+    if (special) {
+        const char* rp = row_ptr(a, r);
+        const uint32_t nw = (hi - lo + 31u) / 32u;
+        for (uint32_t wi = tid; wi < nw; wi += NT_CHUNK) {
+            uint32_t bits = L.spec[wi] | L.ban[wi];
+            while (bits) {
+                const uint32_t b = (uint32_t)__ffs((int)bits) - 1u;
+                bits &= bits - 1u;
+                const uint32_t off = wi * 32u + b;
+                const uint32_t e = lo + off;
+                float l = DT == AXS_DTYPE_BF16 ? __uint_as_float((uint32_t)((const uint16_t*)rp)[e] << 16)
+                                               : ((const float*)rp)[e];
+                if ((L.spec[wi] >> b) & 1u)
+                    l = proc_special(a.hist, L, off, e, l, pfl, c.p.repetition_penalty,
+                                     c.p.frequency_penalty, c.p.presence_penalty, c.w0, c.w1);
+                if (c.mask_on) {
+                    uint32_t mw = a.mask[(size_t)r * a.mask_stride + (e >> 5)];
+                    if (!((mw >> (e & 31u)) & 1u)) l = -INFINITY;
+                }
+                if ((L.ban[wi] >> b) & 1u) l = -INFINITY;
+                f(e, l);
+            }
+        }
+    }
 }
 
 // XCD-aware work-item mapping: the hardware hands workgroup b to XCD b % 8;
-// give each XCD a contiguous range of (row, chunk) items so the chunks of a
-// row share one L2.
+// give each XCD a contiguous range of (row, segment) items so the segments of
+// a row share one L2.
 __device__ __forceinline__ int64_t xcd_item(int64_t total) {
     int64_t per = (total + 7) / 8;
     int64_t b = blockIdx.x;
     return (b % 8) * per + b / 8;
 }
 
+// wave-aggregated append of a candidate into LDS (one LDS atomic per wave)
+__device__ __forceinline__ void cand_append(bool in, uint32_t id, float l, uint32_t* s_n, Cand* s_cand) {
+    const int lane = threadIdx.x & 63;
+    uint64_t m = __ballot(in);
+    if (m == 0ull) return;
+    uint32_t base = 0;
+    int leader = __ffsll((long long)m) - 1;
+    if (lane == leader) base = atomicAdd(s_n, (uint32_t)__popcll(m));
+    base = (uint32_t)__shfl((int)base, leader, 64);
+    if (in) {
+        uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+        if (slot < CAPC) {
+            s_cand[slot].id = id;
+            s_cand[slot].l = l;
+        }
+    }
+}
+
 // --------------------------------------------------------------------------
-// k_chunk
+// k_chunk: the single pass over the logits, one segment per workgroup
 // --------------------------------------------------------------------------
-template <int DT, int NV, bool VEC>
+template <int DT, int NV>
 __global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
-    constexpr int EPV = DT == AXS_DTYPE_BF16 ? 8 : 4;
-    constexpr int EPT = NV * EPV;
     __shared__ ProcLds L;
     __shared__ Cand s_cand[CAPC];
     __shared__ uint32_t s_hist[NBIN];
@@ -477,19 +595,16 @@ __global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
     const uint32_t hi = min(lo + (uint32_t)a.chunk, (uint32_t)a.vocab);
 
     RowCtx c = make_ctx(a, r);
+    Seg<DT, NV> S;
+    seg_load<DT, NV>(a, r, lo, hi, a.vec != 0, c.mask_on, S);  // in flight during the setup
     if (c.any_proc) proc_setup(a, c, lo, hi, L);
-
-    float v[EPT];
-    load_chunk<DT, NV, VEC>(a, c, L, r, lo, hi, v);
 
     // max and first argmax (NaN skipped)
     float bm = -INFINITY;
     uint32_t bi = NONE;
-#pragma unroll
-    for (int k = 0; k < EPT; ++k) {
-        float x = v[k];
-        if (!isnan(x)) am_merge(bm, bi, x, elem_id<DT, NV>(lo, k));
-    }
+    seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
+        if (!isnan(l)) am_merge(bm, bi, l, e);
+    });
     block_argmax<NT_CHUNK>(bm, bi, s_f, s_u);
     const float mc = bi == NONE ? -INFINITY : bm;
 
@@ -506,16 +621,16 @@ __global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
     if (mode == M_GREEDY) {
         if (a.want_logprob && isfinite(mc)) {
             float s = 0.0f;
-#pragma unroll
-            for (int k = 0; k < EPT; ++k)
-                if (isfinite(v[k])) s += __expf(v[k] - mc);
+            seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t, float l) {
+                if (isfinite(l)) s += __expf(l - mc);
+            });
             st.gsum = block_sum_f<NT_CHUNK>(s, s_f);
         }
     } else if ((mode == M_MINP || mode == M_TOPK) && isfinite(mc)) {
         const float inv = __fdiv_rn(1.0f, c.p.temperature);
         if (isfinite(inv)) {
             if (tid == 0) s_n = 0;
-            bool use_bins = mode == M_TOPK;
+            const bool use_bins = mode == M_TOPK;
             uint32_t bstar = 0;
             float thr = 0.0f;
             if (use_bins) {
@@ -524,11 +639,10 @@ __global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
                 } else {
                     for (uint32_t i = tid; i < NBIN; i += NT_CHUNK) s_hist[i] = 0;
                     __syncthreads();
-#pragma unroll
-                    for (int k = 0; k < EPT; ++k) {
-                        float x = __fmul_rn(__fsub_rn(mc, v[k]), inv);
+                    seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t, float l) {
+                        float x = __fmul_rn(__fsub_rn(mc, l), inv);
                         if (x < 64.0f) atomicAdd(&s_hist[(uint32_t)(x * 32.0f)], 1u);
-                    }
+                    });
                     __syncthreads();
                     uint32_t loc = 0;
 #pragma unroll
@@ -561,29 +675,22 @@ __global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
             } else {
                 thr = __fsub_rn(ln_f32(c.p.min_p), 1e-3f);
             }
+            __syncthreads();
             if (!(st.flags & CS_OVERFLOW)) {
                 float lx = -INFINITY;
-#pragma unroll
-                for (int k = 0; k < EPT; ++k) {
-                    float l = v[k];
-                    if (isnan(l)) continue;
-                    bool in;
-                    if (use_bins) {
-                        float x = __fmul_rn(__fsub_rn(mc, l), inv);
-                        in = x < 64.0f && (uint32_t)(x * 32.0f) <= bstar;
-                    } else {
-                        in = __fmul_rn(__fsub_rn(l, mc), inv) >= thr;
-                    }
-                    if (in) {
-                        uint32_t slot = atomicAdd(&s_n, 1u);
-                        if (slot < CAPC) {
-                            s_cand[slot].id = elem_id<DT, NV>(lo, k);
-                            s_cand[slot].l = l;
+                seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
+                    bool in = false;
+                    if (!isnan(l)) {
+                        if (use_bins) {
+                            float x = __fmul_rn(__fsub_rn(mc, l), inv);
+                            in = x < 64.0f && (uint32_t)(x * 32.0f) <= bstar;
+                        } else {
+                            in = __fmul_rn(__fsub_rn(l, mc), inv) >= thr;
                         }
-                    } else {
-                        lx = fmaxf(lx, l);
+                        if (!in) lx = fmaxf(lx, l);
                     }
-                }
+                    cand_append(in, e, l, &s_n, s_cand);
+                });
                 lx = block_max<NT_CHUNK>(lx, s_f);
                 uint32_t n = s_n;
                 if (n > CAPC) {
@@ -599,7 +706,6 @@ __global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
     }
     if (tid == 0) a.cstat[(size_t)r * a.nch + ci] = st;
 }
-
 // --------------------------------------------------------------------------
 // outputs
 // --------------------------------------------------------------------------
@@ -638,6 +744,7 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
     __shared__ double s_d[NT_FIN / 64];
     __shared__ uint32_t s_n;
     __shared__ float s_mg;
+    __shared__ uint32_t s_coff[MAX_SEGS + 1];
     const int r = blockIdx.x;
     const int tid = threadIdx.x;
     if (r >= a.nrows) return;
@@ -719,11 +826,36 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
         }
         __syncthreads();
         float mg = INFINITY;
-        for (int c = 0; c < nch; ++c) {
-            uint32_t cnt = a.cstat[(size_t)r * nch + c].count;
-            const Cand* src = a.cand + ((size_t)r * nch + c) * CAPC;
-            for (uint32_t i = tid; i < cnt; i += NT_FIN) {
-                Cand cd = src[i];
+        // candidate counts of every segment → prefix offsets, then one flat
+        // parallel loop over all candidates of the row
+        uint32_t loc = 0;
+        constexpr uint32_t PER = MAX_SEGS / NT_FIN;
+        for (uint32_t q = 0; q < PER; ++q) {
+            uint32_t c = (uint32_t)tid * PER + q;
+            uint32_t cnt = c < (uint32_t)nch ? a.cstat[(size_t)r * nch + c].count : 0u;
+            s_coff[c] = cnt;
+            loc += cnt;
+        }
+        uint32_t ntot;
+        uint32_t pre = block_excl_scan_u32<NT_FIN>(loc, s_u, &ntot);
+        for (uint32_t q = 0; q < PER; ++q) {
+            uint32_t c = (uint32_t)tid * PER + q;
+            uint32_t cnt = s_coff[c];
+            s_coff[c] = pre;
+            pre += cnt;
+        }
+        if (tid == 0) s_coff[MAX_SEGS] = ntot;
+        __syncthreads();
+        for (uint32_t i = tid; i < ntot; i += NT_FIN) {
+            uint32_t lo_c = 0, hi_c = (uint32_t)nch;  // last c with s_coff[c] <= i
+            while (hi_c - lo_c > 1) {
+                uint32_t mid = (lo_c + hi_c) / 2;
+                if (s_coff[mid] <= i) lo_c = mid;
+                else hi_c = mid;
+            }
+            {
+                const uint32_t c = lo_c;
+                Cand cd = a.cand[((size_t)r * nch + c) * CAPC + (i - s_coff[c])];
                 if (!(cd.l > lx)) continue;
                 float pr = prob_of(cd.l, m, inv);
                 uint64_t key;
@@ -793,7 +925,10 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
             if (sorted && (kept < L || mode == M_TOPK)) {
                 float nextp = kept < L ? P(kept) : -1.0f;
                 if (mode == M_TOPK) nextp = fmaxf(nextp, plx);
-                if (nextp >= 0.0f && (double)P(kept - 1) - (double)nextp <= 2.0 * ulp_f(P(kept - 1)))
+                // near but not identical probabilities across the cut (identical
+                // ones come from equal logits and are ordered by id everywhere)
+                if (nextp >= 0.0f && P(kept - 1) != nextp &&
+                    (double)P(kept - 1) - (double)nextp <= 2.0 * ulp_f(P(kept - 1)))
                     flags |= AXS_FLAG_NEAR_TIE;
             }
             float F = 0.0f;
@@ -867,10 +1002,8 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
 // --------------------------------------------------------------------------
 // k_exact_mat: exact probabilities of the listed rows (second pass)
 // --------------------------------------------------------------------------
-template <int DT, int NV, bool VEC>
+template <int DT, int NV>
 __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
-    constexpr int EPV = DT == AXS_DTYPE_BF16 ? 8 : 4;
-    constexpr int EPT = NV * EPV;
     __shared__ ProcLds L;
     __shared__ uint32_t s_u[NT_CHUNK / 64];
     __shared__ float s_f[NT_CHUNK / 64];
@@ -885,41 +1018,43 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
         const uint32_t hi = min(lo + (uint32_t)a.chunk, (uint32_t)a.vocab);
         const RowState rs = a.rstate[r];
         RowCtx c = make_ctx(a, r);
+        Seg<DT, NV> S;
+        seg_load<DT, NV>(a, r, lo, hi, a.vec != 0, c.mask_on, S);
         if (c.any_proc) proc_setup(a, c, lo, hi, L);
-        float v[EPT];
-        load_chunk<DT, NV, VEC>(a, c, L, r, lo, hi, v);
         const bool minp = rs.mode == M_MINP;
         const float minp_v = c.p.min_p;
         float mg = INFINITY;
         uint32_t cnt = 0;
-#pragma unroll
-        for (int k = 0; k < EPT; ++k) {
-            float pr = prob_of(v[k], rs.m, rs.inv);
+        float* dense = a.dense + (size_t)r * a.vocab;
+        // pass 1: exact probabilities; dense rows are written here, sorted rows
+        // only counted
+        seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
+            float pr = prob_of(l, rs.m, rs.inv);
             bool keep = true;
             if (minp) {
-                if (!isnan(v[k])) mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
+                if (!isnan(l)) mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
                 keep = pr >= minp_v;
             }
-            v[k] = keep ? pr : 0.0f;
-            if (rs.sorted && v[k] >= rs.pmin) ++cnt;
-        }
-        if (!rs.sorted) {
-            float* dst = a.dense + (size_t)r * a.vocab;
-#pragma unroll
-            for (int k = 0; k < EPT; ++k) {
-                uint32_t e = elem_id<DT, NV>(lo, k);
-                if (e < hi) dst[e] = v[k];
+            float v = keep ? pr : 0.0f;
+            if (!rs.sorted) {
+                if (e < hi) dense[e] = v;
+            } else if (v >= rs.pmin) {
+                ++cnt;
             }
-        } else {
+        });
+        if (rs.sorted) {
             uint32_t tot;
             uint32_t pre = block_excl_scan_u32<NT_CHUNK>(cnt, s_u, &tot);
             if (tid == 0) s_base = tot ? atomicAdd(&a.rstate[r].ncompact, tot) : 0u;
             __syncthreads();
             uint64_t* dst = a.ckey + (size_t)r * a.vocab + s_base + pre;
             uint32_t o = 0;
-#pragma unroll
-            for (int k = 0; k < EPT; ++k)
-                if (v[k] >= rs.pmin) dst[o++] = key_pdesc(v[k], elem_id<DT, NV>(lo, k));
+            // pass 2: write the compacted (p desc, id asc) keys
+            seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
+                float pr = prob_of(l, rs.m, rs.inv);
+                if (minp && !(pr >= minp_v)) pr = 0.0f;
+                if (pr >= rs.pmin) dst[o++] = key_pdesc(pr, e);
+            });
         }
         if (minp) {
             mg = block_max<NT_CHUNK>(-mg, s_f);
@@ -1181,7 +1316,7 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
         Lk = kept < L ? kept : L;
         if (kept < L) {
             float pa = pdesc_p(keys[kept - 1]), pb = pdesc_p(keys[kept]);
-            if ((double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
+            if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
         }
         F = S[Lk - 1];
         const float thr = __fmul_rn(rs.u, F);
@@ -1478,11 +1613,13 @@ struct axs_context {
     uint32_t* kept_id;
     float* kept_p;
     uint32_t* mtp_tok;  // per-row tokens of the MTP sampler pass
+    bool timing;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> ev[AXS_KERNEL_COUNT];
 };
 
 namespace {
 
-constexpr uint32_t MIN_CHUNK = 2048;
+constexpr uint32_t MIN_CHUNK = 2048;  // smallest segment (bf16 x1, f32 x2)
 
 struct DevGuard {
     int prev = -1;
@@ -1505,7 +1642,10 @@ int dalloc(T** p, size_t n) {
     return AXS_OK;
 }
 
+void clear_events(axs_context* c);
+
 void free_ctx(axs_context* c) {
+    clear_events(c);
     void* ptrs[] = {c->cstat, c->cand,  c->rstate, c->exact_rows, c->exact_count, c->dense,  c->ckey,
                     c->ckey2, c->tmp64, c->sbuf,   c->bend,       c->kept_id,     c->kept_p, c->mtp_tok};
     for (void* q : ptrs)
@@ -1521,19 +1661,31 @@ struct Plan {
     bool vec;
 };
 
+// Segment size: the largest per-thread vector count whose grid still has
+// >= 1024 workgroups (four per CU), so each workgroup keeps up to 64 KB of
+// loads in flight while the GPU stays full.
 Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride, const void* base2) {
     const int epv = dtype == AXS_DTYPE_BF16 ? 8 : 4;
     const int es = dtype == AXS_DTYPE_BF16 ? 2 : 4;
-    int nvs_bf16[3] = {4, 2, 1};
-    int nvs_f32[3] = {8, 4, 2};
-    int* nvs = dtype == AXS_DTYPE_BF16 ? nvs_bf16 : nvs_f32;
+    static const int nvs_bf16[5] = {16, 8, 4, 2, 1};
+    static const int nvs_f32[4] = {16, 8, 4, 2};
+    const int* nvs = dtype == AXS_DTYPE_BF16 ? nvs_bf16 : nvs_f32;
+    const int nn = dtype == AXS_DTYPE_BF16 ? 5 : 4;
+    // AXS_SEG_NV_MAX caps the vectors per thread (tuning; default 8)
+    static const int nv_cap = [] {
+        const char* e = getenv("AXS_SEG_NV_MAX");
+        int v = e ? atoi(e) : 8;
+        return v >= 1 ? v : 8;
+    }();
     Plan pl;
-    pl.nv = nvs[2];
-    for (int i = 0; i < 3; ++i) {
+    pl.nv = nvs[nn - 1];
+    for (int i = 0; i < nn; ++i) {
+        if (nvs[i] > nv_cap && i + 1 < nn) continue;
         uint32_t ch = (uint32_t)(NT_CHUNK * nvs[i] * epv);
-        int nch = (int)((vocab + ch - 1) / ch);
+        int64_t nch = ((int64_t)vocab + ch - 1) / ch;
+        if (nch > (int64_t)MAX_SEGS) break;  // keep the previous (larger) segment
         pl.nv = nvs[i];
-        if ((int64_t)nrows * nch >= 2048) break;
+        if ((int64_t)nrows * nch >= 1024) break;
     }
     pl.chunk = (uint32_t)(NT_CHUNK * pl.nv * epv);
     pl.nch = (int)((vocab + pl.chunk - 1) / pl.chunk);
@@ -1543,30 +1695,61 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
 }
 
 template <int DT, int NV>
-void launch_pair_nv(const Plan& pl, const KArgs& a, hipStream_t s, bool exact_pass) {
+void launch_pair_nv(const KArgs& a, hipStream_t s, bool exact_pass) {
     const int64_t total = (int64_t)a.nrows * a.nch;
     if (!exact_pass) {
         dim3 grid((unsigned)(((total + 7) / 8) * 8));
-        if (pl.vec) hipLaunchKernelGGL((k_chunk<DT, NV, true>), grid, dim3(NT_CHUNK), 0, s, a);
-        else hipLaunchKernelGGL((k_chunk<DT, NV, false>), grid, dim3(NT_CHUNK), 0, s, a);
+        hipLaunchKernelGGL((k_chunk<DT, NV>), grid, dim3(NT_CHUNK), 0, s, a);
     } else {
-        int64_t g = total < 2048 ? total : 2048;
+        int64_t g = total < 1024 ? total : 1024;
         dim3 grid((unsigned)(g > 0 ? g : 1));
-        if (pl.vec) hipLaunchKernelGGL((k_exact_mat<DT, NV, true>), grid, dim3(NT_CHUNK), 0, s, a);
-        else hipLaunchKernelGGL((k_exact_mat<DT, NV, false>), grid, dim3(NT_CHUNK), 0, s, a);
+        hipLaunchKernelGGL((k_exact_mat<DT, NV>), grid, dim3(NT_CHUNK), 0, s, a);
     }
 }
 
 void launch_chunkish(const Plan& pl, const KArgs& a, hipStream_t s, bool exact_pass) {
     if (a.dtype == AXS_DTYPE_BF16) {
-        if (pl.nv == 4) launch_pair_nv<AXS_DTYPE_BF16, 4>(pl, a, s, exact_pass);
-        else if (pl.nv == 2) launch_pair_nv<AXS_DTYPE_BF16, 2>(pl, a, s, exact_pass);
-        else launch_pair_nv<AXS_DTYPE_BF16, 1>(pl, a, s, exact_pass);
+        switch (pl.nv) {
+            case 16: launch_pair_nv<AXS_DTYPE_BF16, 16>(a, s, exact_pass); break;
+            case 8: launch_pair_nv<AXS_DTYPE_BF16, 8>(a, s, exact_pass); break;
+            case 4: launch_pair_nv<AXS_DTYPE_BF16, 4>(a, s, exact_pass); break;
+            case 2: launch_pair_nv<AXS_DTYPE_BF16, 2>(a, s, exact_pass); break;
+            default: launch_pair_nv<AXS_DTYPE_BF16, 1>(a, s, exact_pass); break;
+        }
     } else {
-        if (pl.nv == 8) launch_pair_nv<AXS_DTYPE_F32, 8>(pl, a, s, exact_pass);
-        else if (pl.nv == 4) launch_pair_nv<AXS_DTYPE_F32, 4>(pl, a, s, exact_pass);
-        else launch_pair_nv<AXS_DTYPE_F32, 2>(pl, a, s, exact_pass);
+        switch (pl.nv) {
+            case 16: launch_pair_nv<AXS_DTYPE_F32, 16>(a, s, exact_pass); break;
+            case 8: launch_pair_nv<AXS_DTYPE_F32, 8>(a, s, exact_pass); break;
+            case 4: launch_pair_nv<AXS_DTYPE_F32, 4>(a, s, exact_pass); break;
+            default: launch_pair_nv<AXS_DTYPE_F32, 2>(a, s, exact_pass); break;
+        }
     }
+}
+
+void clear_events(axs_context* c) {
+    for (auto& v : c->ev) {
+        for (auto& e : v) {
+            (void)hipEventDestroy(e.first);
+            (void)hipEventDestroy(e.second);
+        }
+        v.clear();
+    }
+}
+
+// Brackets one launch with events on its stream when timing is enabled.
+template <typename F>
+void timed(axs_context* c, int kind, hipStream_t s, F&& launch) {
+    if (!c->timing) {
+        launch();
+        return;
+    }
+    hipEvent_t a = nullptr, b = nullptr;
+    (void)hipEventCreate(&a);
+    (void)hipEventCreate(&b);
+    (void)hipEventRecord(a, s);
+    launch();
+    (void)hipEventRecord(b, s);
+    c->ev[kind].push_back({a, b});
 }
 
 void fill_ws(KArgs& a, axs_context* c) {
@@ -1586,13 +1769,19 @@ void fill_ws(KArgs& a, axs_context* c) {
 
 // the four-kernel pipeline over a.nrows rows
 int run_pipeline(axs_context* c, KArgs& a, const Plan& pl, hipStream_t s) {
+    if (pl.nch > (int)MAX_SEGS) return fail(AXS_E_UNSUPPORTED, "vocab too large (more than 1024 segments)");
     a.nch = pl.nch;
     a.chunk = (int32_t)pl.chunk;
+    a.vec = pl.vec ? 1 : 0;
     fill_ws(a, c);
-    launch_chunkish(pl, a, s, false);
-    hipLaunchKernelGGL(k_finish, dim3((unsigned)a.nrows), dim3(NT_FIN), 0, s, a);
-    launch_chunkish(pl, a, s, true);
-    hipLaunchKernelGGL(k_exact_row, dim3((unsigned)a.nrows), dim3(NT_EX), 0, s, a);
+    timed(c, AXS_KERNEL_CHUNK, s, [&] { launch_chunkish(pl, a, s, false); });
+    timed(c, AXS_KERNEL_FINISH, s, [&] {
+        hipLaunchKernelGGL(k_finish, dim3((unsigned)a.nrows), dim3(NT_FIN), 0, s, a);
+    });
+    timed(c, AXS_KERNEL_EXACT_MAT, s, [&] { launch_chunkish(pl, a, s, true); });
+    timed(c, AXS_KERNEL_EXACT_ROW, s, [&] {
+        hipLaunchKernelGGL(k_exact_row, dim3((unsigned)a.nrows), dim3(NT_EX), 0, s, a);
+    });
     AXS_HIP_CHECK(hipGetLastError());
     return AXS_OK;
 }
@@ -1722,12 +1911,16 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
     a.out_ids = out_ids;
     a.out_lp = out_logprob;
     Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
+    if (pl.nch > (int)MAX_SEGS) return fail(AXS_E_UNSUPPORTED, "vocab too large (more than 1024 segments)");
     a.nch = pl.nch;
     a.chunk = (int32_t)pl.chunk;
+    a.vec = pl.vec ? 1 : 0;
     fill_ws(a, ctx);
     hipStream_t s = (hipStream_t)stream;
-    launch_chunkish(pl, a, s, false);
-    hipLaunchKernelGGL(k_finish, dim3((unsigned)batch), dim3(NT_FIN), 0, s, a);
+    timed(ctx, AXS_KERNEL_CHUNK, s, [&] { launch_chunkish(pl, a, s, false); });
+    timed(ctx, AXS_KERNEL_FINISH, s, [&] {
+        hipLaunchKernelGGL(k_finish, dim3((unsigned)batch), dim3(NT_FIN), 0, s, a);
+    });
     AXS_HIP_CHECK(hipGetLastError());
     return AXS_OK;
 }
@@ -1764,9 +1957,35 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_output
     Plan pl = make_plan(d->dtype, (int)rows, d->vocab, d->target_logits, d->row_stride, d->draft_logits);
     int rc = run_pipeline(ctx, a, pl, s);
     if (rc) return rc;
-    hipLaunchKernelGGL(k_mtp_verify, dim3((unsigned)d->batch), dim3(256), 0, s, a, d->draft_ids,
-                       o->out_ids, o->out_count, o->accept_count, o->flags);
+    timed(ctx, AXS_KERNEL_MTP, s, [&] {
+        hipLaunchKernelGGL(k_mtp_verify, dim3((unsigned)d->batch), dim3(256), 0, s, a, d->draft_ids,
+                           o->out_ids, o->out_count, o->accept_count, o->flags);
+    });
     AXS_HIP_CHECK(hipGetLastError());
+    return AXS_OK;
+}
+
+int axs_timing_enable(axs_context* ctx, int enable) {
+    if (!ctx) return fail(AXS_E_INVALID, "ctx is NULL");
+    DevGuard g(ctx->device);
+    clear_events(ctx);
+    ctx->timing = enable != 0;
+    return AXS_OK;
+}
+
+int axs_timing_read(axs_context* ctx, int kernel, double* total_ms, int* launches) {
+    if (!ctx || !total_ms || !launches) return fail(AXS_E_INVALID, "NULL argument");
+    if (kernel < 0 || kernel >= AXS_KERNEL_COUNT) return fail(AXS_E_INVALID, "bad kernel id");
+    DevGuard g(ctx->device);
+    double t = 0.0;
+    for (auto& e : ctx->ev[kernel]) {
+        AXS_HIP_CHECK(hipEventSynchronize(e.second));
+        float ms = 0.0f;
+        AXS_HIP_CHECK(hipEventElapsedTime(&ms, e.first, e.second));
+        t += ms;
+    }
+    *total_ms = t;
+    *launches = (int)ctx->ev[kernel].size();
     return AXS_OK;
 }
 

@@ -227,6 +227,20 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
                    const axs_mtp_outputs* out, void* stream);
 
+/* Per-kernel timing, for benchmarks (no counterpart in the reference).  While
+ * enabled, every kernel the context launches is bracketed by hipEvents
+ * recorded on its launch stream.  Enabling clears earlier records. */
+#define AXS_KERNEL_CHUNK     0  /* the single pass over the logits    */
+#define AXS_KERNEL_FINISH    1  /* per-row merge and decisions        */
+#define AXS_KERNEL_EXACT_MAT 2  /* exact path: second pass            */
+#define AXS_KERNEL_EXACT_ROW 3  /* exact path: sort + exact sums      */
+#define AXS_KERNEL_MTP       4  /* MTP accept / residual / bonus      */
+#define AXS_KERNEL_COUNT     5
+int axs_timing_enable(axs_context* ctx, int enable);
+/* Waits for the recorded events of one kernel class and returns their summed
+ * duration in milliseconds and the number of launches since enabling. */
+int axs_timing_read(axs_context* ctx, int kernel, double* total_ms, int* launches);
+
 #ifdef __cplusplus
 }
 #endif

@@ -296,7 +296,7 @@ static double ulp_of(float x) {
 /* apply_top_k_top_p (sampling.rs:922-952), recording the nucleus margins. */
 static uint32_t apply_top_k_top_p(uint32_t* cid, float* cp, uint32_t n, uint32_t top_k,
                                   float top_p, workspace* w, axo_explain* ex,
-                                  int* sorted) {
+                                  int* sorted, const float* L) {
     *sorted = 0;
     int filters_enabled = top_k > 0 || top_p < 1.0f;
     if (!filters_enabled) {
@@ -337,7 +337,11 @@ static uint32_t apply_top_k_top_p(uint32_t* cid, float* cp, uint32_t n, uint32_t
     if (ex) {
         if (ex->margin_nucleus < 1e-6 && (top_k == 0 || keep_n <= top_k))
             ex->boundary |= AXS_FLAG_NEAR_NUCLEUS;
-        if (kept < n) {
+        /* probabilities within 2 ulp across the cut, from DIFFERENT logits:
+         * a one-ulp difference between two exp implementations could swap
+         * them.  Equal logits give equal probabilities everywhere and are
+         * ordered by id on both sides, so they are not a boundary. */
+        if (kept < n && L && L[cid[kept - 1]] != L[cid[kept]]) {
             double d = (double)cp[kept - 1] - (double)cp[kept];
             double u = ulp_of(cp[kept - 1]);
             ex->margin_tie = u > 0 ? d / u : INFINITY;
@@ -510,7 +514,7 @@ static uint32_t sample_row_ws(const float* logits, uint32_t V, const axs_samplin
     }
     ex->n_cand = n;
     int sorted = 0;
-    uint32_t kept = apply_top_k_top_p(w->cid, w->cp, n, p->top_k, p->top_p, w, ex, &sorted);
+    uint32_t kept = apply_top_k_top_p(w->cid, w->cp, n, p->top_k, p->top_p, w, ex, &sorted, L);
     ex->sorted = (uint32_t)sorted;
     ex->n_kept = kept;
     float F = 0.0f;                               /* :297-300 */
@@ -696,7 +700,7 @@ static int token_distribution_ws(const float* logits, uint32_t V, const axs_samp
     }
     int sorted = 0;
     if (p->top_k > 0 || p->top_p < 1.0f)
-        n = apply_top_k_top_p(w->cid, w->cp, n, p->top_k, p->top_p, w, NULL, &sorted);
+        n = apply_top_k_top_p(w->cid, w->cp, n, p->top_k, p->top_p, w, NULL, &sorted, NULL);
     float fs = 0.0f;
     for (uint32_t i = 0; i < n; ++i) fs += w->cp[i];
     if (fs == 0.0f || !isfinite(fs))

@@ -65,7 +65,13 @@ def test_argmax_batch_matches_oracle(sampler, oracle):
             assert ids[r] == oracle.argmax_f32(xf[r]), (dt, V, r)
             core = oracle.core_argmax_logprob(xf[r], pack_params([MlxSamplingParams()]))
             if core is not None:
-                assert abs(lp[r] - core[1]) <= 1e-5 * max(1.0, abs(core[1])), (r, lp[r], core)
+                # -ln sum exp(l - max) against its float64 value: the core
+                # sampler's sequential f32 sum itself drifts by ~1e-4 relative
+                # over 1.5e5 terms, so it is only held to 1e-3
+                l64 = xf[r][np.isfinite(xf[r])].astype(np.float64)
+                want = -math.log(np.sum(np.exp(l64 - l64.max())))
+                assert abs(lp[r] - want) <= 1e-5 * max(1.0, abs(want)), (r, lp[r], want)
+                assert abs(lp[r] - core[1]) <= 1e-3 * max(1.0, abs(core[1])), (r, lp[r], core)
 
 
 @pytest.mark.parametrize("seed", [1, 2, 3])
