@@ -60,8 +60,8 @@ EXPORTS = (
     "axs_timing_read",
 )
 
-KERNEL_CHUNK, KERNEL_FINISH, KERNEL_EXACT_MAT, KERNEL_EXACT_ROW, KERNEL_MTP = range(5)
-KERNEL_NAMES = ("k_chunk", "k_finish", "k_exact_mat", "k_exact_row", "k_mtp_verify")
+KERNEL_STREAM, KERNEL_EXACT_MAT, KERNEL_EXACT_ROW, KERNEL_MTP = range(4)
+KERNEL_NAMES = ("k_stream", "k_exact_mat", "k_exact_row", "k_mtp_verify")
 
 
 def build_library(verbose: bool = False) -> str:

@@ -234,6 +234,20 @@ __device__ __forceinline__ double block_sum_d(double v, double* sv) {
 }
 
 template <int NT>
+__device__ __forceinline__ uint32_t block_min_u32(uint32_t v, uint32_t* sv) {
+    constexpr int NW = NT / 64;
+    v = wave_min_u32(v);
+    int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) sv[w] = v;
+    __syncthreads();
+    v = sv[0];
+#pragma unroll
+    for (int k = 1; k < NW; ++k) v = min(v, sv[k]);
+    __syncthreads();
+    return v;
+}
+
+template <int NT>
 __device__ __forceinline__ float block_sum_f(float v, float* sv) {
     constexpr int NW = NT / 64;
     v = wave_sum_f(v);
@@ -326,6 +340,42 @@ __device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
         }
     }
     return key;
+}
+
+// Descending bitonic sort of 256 u64 keys held four per lane by one wave:
+// element i = j * 64 + lane is k[j].
+__device__ __forceinline__ void wave_sort_desc4(uint64_t k[4]) {
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int size = 2; size <= 256; size <<= 1) {
+#pragma unroll
+        for (int d = size >> 1; d > 0; d >>= 1) {
+            if (d >= 64) {
+                const int dj = d >> 6;
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    if (j & dj) continue;  // each pair (j, j + dj) once
+                    const int j2 = j | dj;
+                    const bool desc = ((j * 64 + lane) & size) == 0;
+                    const uint64_t x = k[j], y = k[j2];
+                    const bool swap = desc ? (x < y) : (x > y);
+                    k[j] = swap ? y : x;
+                    k[j2] = swap ? x : y;
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const int i = j * 64 + lane;
+                    const uint64_t o = shfl_xor_u64(k[j], d);
+                    const bool desc = (i & size) == 0;
+                    const bool lower = (i & d) == 0;
+                    const uint64_t mx = k[j] > o ? k[j] : o;
+                    const uint64_t mn = k[j] > o ? o : k[j];
+                    k[j] = (desc == lower) ? mx : mn;
+                }
+            }
+        }
+    }
 }
 
 // Descending bitonic sort of n (a power of two) keys in memory `s` (LDS or

@@ -1,20 +1,20 @@
 // axs_sampler.hip — MI355X (gfx950) per-step token sampler behind the C ABI
 // of include/ax_hip_sampler.h.
 //
-// One sampling step over [rows, V] logits in HBM runs as four kernels on the
+// One sampling step over [rows, V] logits in HBM runs as three kernels on the
 // caller's stream:
 //
-//   k_chunk     one pass over the logits (the HBM-bound kernel).  Work item =
-//               (row, chunk of <= 8192 ids); the chunks of a row are placed on
-//               one XCD.  Per chunk: the logits processors (repetition,
-//               presence/frequency, bias, mask, n-gram ban) from LDS tables,
-//               max/argmax, and — for min-p and top-k rows — every element
-//               that can still be in the row's kept set, plus the largest
-//               value it left out.
-//   k_finish    one workgroup per row.  Merges the chunk results; greedy,
-//               fallback, min-p and top-k rows are decided here exactly when
-//               the gathered candidates provably contain the needed prefix.
-//               Other rows join the exact-path list.
+//   k_stream    the single pass over the logits (the HBM-bound kernel).  Work
+//               item = (row, segment of <= 65536 ids); the segments of a row
+//               are placed on one XCD.  Each workgroup builds the logits
+//               processors' LDS tables for its segment (repetition,
+//               presence/frequency, bias, mask, n-gram ban) while its first
+//               tiles load, then streams the segment in double-buffered
+//               register tiles: max/argmax, and for min-p rows every id within
+//               the min-p window of the running maximum.  The last workgroup
+//               of a row to finish decides the row in place (greedy, fallback,
+//               min-p rows whose survivors were gathered) or lists it for
+//               the exact path.
 //   k_exact_mat exact path, pass 2 over the listed rows: exact probabilities
 //               with the global max, written dense (index-order laws) or
 //               compacted (sorted laws).
@@ -35,6 +35,7 @@
 
 #include <cstdlib>
 #include <mutex>
+#include <type_traits>
 #include <new>
 #include <string>
 #include <vector>
@@ -47,15 +48,16 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NT_CHUNK = 256;
-constexpr uint32_t SEG_MAX = 32768;   // ids per segment (upper bound)
+constexpr uint32_t SEG_MAX = 65536;   // ids per k_stream segment, 256-thread workgroups
+constexpr uint32_t ROW_MAX = 262144;  // ids per row, one 1024-thread workgroup per row
+constexpr uint32_t EX_SEGMAX = 32768; // ids per exact-path segment
 constexpr uint32_t MAX_SEGS = 1024;   // segments per row (upper bound)
-constexpr uint32_t CAPC = 512;        // candidates kept per chunk
 constexpr int NT_FIN = 256;
-constexpr uint32_t FIN_CAP = 2048;    // candidates merged per row in k_finish
+constexpr uint32_t FIN_CAP = 2048;    // min-p candidates merged per row
+constexpr uint32_t CAPS = 256;        // published candidates per segment (power of 2)
 constexpr int NT_EX = 1024;
 constexpr uint32_t NBUCKET = 13312;   // 13 per thread; covers p in [2^-24, 1]
 constexpr uint32_t BIAS_LDS = 256;    // bias entries per chunk
-constexpr uint32_t NBIN = 2048;       // top-k histogram bins (1/32 nat each)
 constexpr uint32_t KEPT_CAP = 2048;   // kept entries per MTP distribution row
 constexpr uint32_t BIG_LDS_SORT = 4096;
 constexpr float P_FLOOR = 0x1p-24f;   // smaller terms never change a sum >= 1
@@ -64,20 +66,62 @@ constexpr float P_FLOOR = 0x1p-24f;   // smaller terms never change a sum >= 1
 constexpr uint32_t CS_OVERFLOW = 1u;
 constexpr uint32_t CS_ERROR = 2u;
 
+// A segment's result, published as two 64-bit words (see pub_u64)
 struct ChunkStat {
-    float m;        // max processed logit (-inf if the chunk has no non-NaN)
+    float m;        // max processed logit (-inf if the segment has no non-NaN)
     uint32_t amax;  // lowest id attaining m, NONE if none
-    float lx;       // largest non-NaN logit NOT gathered (-inf if none)
-    uint32_t count; // gathered candidates
-    uint32_t flags;
     float gsum;     // sum of exp(l - m) over finite l (greedy logprob)
-    uint32_t pad0, pad1;
+    uint32_t flags;  // CS_* in bits 0-7, published candidates in bits 8-31
 };
 
 struct Cand {
     uint32_t id;
     float l;
 };
+
+// Cross-workgroup publication inside one kernel.  Segment results and
+// candidates are written with device-scope stores (write-through to the
+// device coherence point) and read back with device-scope loads, and every
+// writer waits for its stores to complete before the row's arrival counter
+// is bumped; the last arriver therefore reads complete data without a
+// device-wide cache write-back per workgroup.
+__device__ __forceinline__ void pub_u64(void* p, uint64_t v) {
+    __hip_atomic_store((uint64_t*)p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t sub_u64(const void* p) {
+    return __hip_atomic_load((uint64_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint32_t sub_u32(const uint32_t* p) {
+    return __hip_atomic_load((uint32_t*)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub_u32(uint32_t* p, uint32_t v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void pub_cand(Cand* p, Cand c) {
+    pub_u64(p, (uint64_t)c.id | ((uint64_t)__float_as_uint(c.l) << 32));
+}
+__device__ __forceinline__ Cand sub_cand(const Cand* p) {
+    const uint64_t v = sub_u64(p);
+    Cand c;
+    c.id = (uint32_t)v;
+    c.l = __uint_as_float((uint32_t)(v >> 32));
+    return c;
+}
+__device__ __forceinline__ void pub_stat(ChunkStat* p, const ChunkStat& st) {
+    pub_u64(p, (uint64_t)__float_as_uint(st.m) | ((uint64_t)st.amax << 32));
+    pub_u64((char*)p + 8, (uint64_t)__float_as_uint(st.gsum) | ((uint64_t)st.flags << 32));
+}
+__device__ __forceinline__ ChunkStat sub_stat(const ChunkStat* p) {
+    const uint64_t v0 = sub_u64(p), v1 = sub_u64((const char*)p + 8);
+    ChunkStat st;
+    st.m = __uint_as_float((uint32_t)v0);
+    st.amax = (uint32_t)(v0 >> 32);
+    st.gsum = __uint_as_float((uint32_t)v1);
+    st.flags = (uint32_t)(v1 >> 32);
+    return st;
+}
+// waits until every memory operation this thread issued has completed
+__device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
 struct RowState {
     float m;
@@ -103,8 +147,10 @@ struct KArgs {
     int32_t dtype;
     int32_t nrows;
     int32_t vocab;
-    int32_t nch;
-    int32_t chunk;
+    int32_t nch;          // exact-path segments per row ...
+    int32_t chunk;        // ... of this many ids
+    int32_t snch;         // k_stream segments per row ...
+    int32_t schunk;       // ... of this many ids
     int32_t mtp_depth;    // > 0: MTP layout
     int32_t mtp_batch;
     int32_t want_logprob;
@@ -124,10 +170,12 @@ struct KArgs {
     const float* uniforms;
     // workspace
     ChunkStat* cstat;
-    Cand* cand;
+    Cand* pool;             // published candidates [rows, segments, CAPS]
     RowState* rstate;
     uint32_t* exact_rows;
     uint32_t* exact_count;
+    uint32_t* row_done;     // per-row segment counters (atomicInc, wrap to 0)
+    uint32_t* ex_done;      // k_exact_row workgroup counter (atomicInc, wrap to 0)
     float* dense;
     uint64_t* ckey;
     uint64_t* ckey2;
@@ -203,25 +251,33 @@ __device__ __forceinline__ float row_uniform(const KArgs& a, int r, const axs_sa
 
 // --------------------------------------------------------------------------
 // logits processors: per-segment LDS tables
-//   spec  bit per id of the segment: the id has a history count or a bias entry
-//   ban   bit per id: banned by the no-repeat n-gram rule
-//   hash  open-addressing table offset → occurrence count in the repetition
-//         window (only ids that occur); if it ever fills, counts are taken by
-//         scanning the window in HBM for the (few) flagged ids
+//   spec  bit per id of the segment: the id occurs in the repetition window,
+//         has a bias entry or is banned.  These "special" ids are processed
+//         one by one; the streaming passes read them as NaN.
+//   pre   number of special ids before each bitmap word: with a popcount
+//         inside the word, the rank of a special id
+//   sid   the id of each rank
+//   cnt   occurrences in the repetition window, by rank (CNT_BAN: banned by
+//         the no-repeat n-gram rule)
 // --------------------------------------------------------------------------
-constexpr uint32_t HSLOTS = 2048;
-constexpr uint32_t HBITS = 11;
+constexpr uint32_t CNT_BAN = 0x80000000u;
 
+template <int NT, uint32_t SEGMAX>
 struct ProcLds {
-    uint32_t spec[SEG_MAX / 32];
-    uint32_t ban[SEG_MAX / 32];
-    uint32_t hkey[HSLOTS];   // offset + 1, 0 = empty
-    uint32_t hval[HSLOTS];   // occurrence count
-    uint32_t bias_id[BIAS_LDS];
-    float bias_v[BIAS_LDS];
+    static constexpr uint32_t NW = SEGMAX / 32;      // bitmap words
+    static constexpr uint32_t PW = NW / NT;          // bitmap words per thread
+    static constexpr uint32_t RCAP = SEGMAX / 32;    // ranked special ids
+    static constexpr uint32_t BCAP = NT >= 1024 ? 1024u : BIAS_LDS;  // bias entries
+    uint32_t spec[NW];
+    uint16_t pre[NW];
+    uint32_t sid[RCAP];
+    uint32_t cnt[RCAP];
+    uint32_t bias_id[BCAP];
+    float bias_v[BCAP];
+    uint32_t scan[NT / 64];
+    uint32_t nspec;  // special ids in the segment
     uint32_t nbias;
-    uint32_t err;    // bias entries beyond BIAS_LDS in one segment
-    uint32_t hfull;  // the hash filled up
+    uint32_t err;    // bias entries beyond BCAP in one segment
 };
 
 struct RowCtx {
@@ -280,56 +336,86 @@ __device__ __forceinline__ RowCtx make_ctx(const KArgs& a, int r) {
     return c;
 }
 
-__device__ __forceinline__ uint32_t hslot(uint32_t off) { return (off * 2654435761u) >> (32 - HBITS); }
+// The first 2048 tokens of the repetition window, loaded before the segment's
+// logits are waited for so the tables can be built while those stream.
+template <int NT>
+struct HistPre {
+    static constexpr int K = 2048 / NT;
+    uint32_t t[K];
+};
 
-__device__ __forceinline__ void hash_add(ProcLds& L, uint32_t off) {
-    const uint32_t key = off + 1u;
-    uint32_t h = hslot(off);
-    for (uint32_t probe = 0; probe < HSLOTS; ++probe) {
-        uint32_t k = L.hkey[h];
-        if (k == 0u) {
-            uint32_t prev = atomicCAS(&L.hkey[h], 0u, key);
-            k = prev == 0u ? key : prev;
-        }
-        if (k == key) {
-            atomicAdd(&L.hval[h], 1u);
-            return;
-        }
-        h = (h + 1u) & (HSLOTS - 1u);
+template <int NT>
+__device__ __forceinline__ void hist_prefetch(const KArgs& a, const RowCtx& c, HistPre<NT>& hp) {
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int k = 0; k < HistPre<NT>::K; ++k) {
+        const int64_t i = c.w0 + tid + (int64_t)k * NT;
+        hp.t[k] = (c.cnt_on && i < c.w1) ? a.hist[i] : NONE;
     }
-    L.hfull = 1u;
 }
 
-// Builds the segment's LDS tables for ids in [lo, hi).  Block-uniform control.
-__device__ __forceinline__ void proc_setup(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi,
-                                           ProcLds& L) {
+// f(token) for every token of the repetition window, spread over the block
+// (the first round from the prefetched registers)
+template <int NT, typename F>
+__device__ __forceinline__ void hist_each(const KArgs& a, const RowCtx& c, const HistPre<NT>& hp, F&& f) {
+    constexpr int K = HistPre<NT>::K;
+    const int tid = threadIdx.x;
+    for (int64_t base = c.w0; base < c.w1; base += (int64_t)K * NT) {
+        uint32_t t[K];
+#pragma unroll
+        for (int k = 0; k < K; ++k) {
+            const int64_t i = base + tid + (int64_t)k * NT;
+            t[k] = base == c.w0 ? hp.t[k] : (i < c.w1 ? a.hist[i] : NONE);
+        }
+#pragma unroll
+        for (int k = 0; k < K; ++k) f(t[k]);
+    }
+}
+
+// f(t) for every token t in [lo, hi) that the no-repeat n-gram rule bans
+// (logits_with_no_repeat_ngram_in_place, sampling.rs:896-920), spread over
+// the block
+template <int NT, typename F>
+__device__ __forceinline__ void ngram_each(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi, F&& f) {
+    const int64_t nhist = c.w1 - c.h0;
+    const uint32_t ng = c.p.no_repeat_ngram_size;
+    int64_t keep = (int64_t)(c.p.ngram_window > ng ? c.p.ngram_window : ng);
+    if (keep > nhist) keep = nhist;
+    const int64_t hs = c.w1 - keep;
+    const int64_t plen = (int64_t)ng - 1;
+    for (int64_t s = threadIdx.x; s + (int64_t)ng <= keep; s += NT) {
+        bool match = true;
+        for (int64_t j = 0; j < plen; ++j)
+            if (a.hist[hs + s + j] != a.hist[c.w1 - plen + j]) {
+                match = false;
+                break;
+            }
+        if (match) {
+            const uint32_t t = a.hist[hs + s + plen];
+            if (t >= lo && t < hi) f(t);
+        }
+    }
+}
+
+// Marks the segment's special ids (ids in [lo, hi)) and lists its bias
+// entries.  Block-uniform control.
+template <int NT, uint32_t SEGMAX>
+__device__ __forceinline__ void proc_build(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi,
+                                           ProcLds<NT, SEGMAX>& L, const HistPre<NT>& hp) {
     const int tid = threadIdx.x;
     const uint32_t nw = (hi - lo + 31u) / 32u;
     if (tid == 0) {
         L.nbias = 0;
         L.err = 0;
-        L.hfull = 0;
+        L.nspec = 0;
     }
-    for (uint32_t i = tid; i < nw; i += NT_CHUNK) {
-        L.spec[i] = 0u;
-        L.ban[i] = 0u;
-    }
-    if (c.cnt_on)
-        for (uint32_t i = tid; i < HSLOTS; i += NT_CHUNK) {
-            L.hkey[i] = 0u;
-            L.hval[i] = 0u;
-        }
+    for (uint32_t i = tid; i < nw; i += NT) L.spec[i] = 0u;
     __syncthreads();
-    if (c.cnt_on) {
-        for (int64_t i = c.w0 + tid; i < c.w1; i += NT_CHUNK) {
-            uint32_t t = a.hist[i];
-            if (t >= lo && t < hi) {
-                uint32_t off = t - lo;
-                hash_add(L, off);
-                atomicOr(&L.spec[off >> 5], 1u << (off & 31u));
-            }
-        }
-    }
+    auto mark = [&](uint32_t t) { atomicOr(&L.spec[(t - lo) >> 5], 1u << ((t - lo) & 31u)); };
+    if (c.cnt_on)
+        hist_each<NT>(a, c, hp, [&](uint32_t t) {
+            if (t >= lo && t < hi) mark(t);
+        });
     if (c.bias_on && tid < 64) {
         // ordered compaction of the in-range entries (list order is the order
         // the additions are applied in)
@@ -349,27 +435,129 @@ __device__ __forceinline__ void proc_setup(const KArgs& a, const RowCtx& c, uint
             uint32_t pre = __popcll(m & ((1ull << lane) - 1ull));
             if (in) {
                 uint32_t slot = base + pre;
-                if (slot < BIAS_LDS) {
+                if (slot < ProcLds<NT, SEGMAX>::BCAP) {
                     L.bias_id[slot] = t;
                     L.bias_v[slot] = v;
-                    atomicOr(&L.spec[(t - lo) >> 5], 1u << ((t - lo) & 31u));
+                    mark(t);
                 } else {
                     L.err = 1;
                 }
             }
             base += __popcll(m);
         }
-        if (lane == 0) L.nbias = base < BIAS_LDS ? base : BIAS_LDS;
+        if (lane == 0) L.nbias = base < ProcLds<NT, SEGMAX>::BCAP ? base : ProcLds<NT, SEGMAX>::BCAP;
     }
+    if (c.ban_on) ngram_each<NT>(a, c, lo, hi, mark);
+    __syncthreads();
+}
+
+// rank of special id e (offset off in the segment)
+template <int NT, uint32_t SEGMAX>
+__device__ __forceinline__ uint32_t rank_of(const ProcLds<NT, SEGMAX>& L, uint32_t off) {
+    const uint32_t w = off >> 5;
+    return L.pre[w] + (uint32_t)__popc(L.spec[w] & ((1u << (off & 31u)) - 1u));
+}
+
+// Ranks the special ids, lists them by rank, counts the repetition window by
+// rank and flags the banned ones.  Returns false when the segment has more
+// special ids than ranks (they are then resolved one by one from HBM).
+// Block-uniform control.
+template <int NT, uint32_t SEGMAX>
+__device__ __forceinline__ bool proc_rank(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi,
+                                          ProcLds<NT, SEGMAX>& L, const HistPre<NT>& hp) {
+    using PL = ProcLds<NT, SEGMAX>;
+    const int tid = threadIdx.x;
+    const uint32_t nw = (hi - lo + 31u) / 32u;
+    uint32_t pc[PL::PW];
+    uint32_t cnt = 0;
+#pragma unroll
+    for (uint32_t k = 0; k < PL::PW; ++k) {
+        const uint32_t wi = (uint32_t)tid * PL::PW + k;
+        pc[k] = wi < nw ? (uint32_t)__popc(L.spec[wi]) : 0u;
+        cnt += pc[k];
+    }
+    uint32_t n;
+    uint32_t pre = block_excl_scan_u32<NT>(cnt, L.scan, &n);
+    const bool ranked = n <= PL::RCAP;
+#pragma unroll
+    for (uint32_t k = 0; k < PL::PW; ++k) {
+        const uint32_t wi = (uint32_t)tid * PL::PW + k;
+        if (wi < nw) {
+            L.pre[wi] = (uint16_t)(pre < 65535u ? pre : 65535u);
+            if (ranked) {
+                uint32_t bits = L.spec[wi];
+                uint32_t rk = pre;
+                while (bits) {
+                    const uint32_t b = (uint32_t)__ffs((int)bits) - 1u;
+                    bits &= bits - 1u;
+                    L.sid[rk] = lo + wi * 32u + b;
+                    L.cnt[rk] = 0u;
+                    ++rk;
+                }
+            }
+        }
+        pre += pc[k];
+    }
+    if (tid == 0) L.nspec = n;
+    __syncthreads();
+    if (ranked) {
+        if (c.cnt_on)
+            hist_each<NT>(a, c, hp, [&](uint32_t t) {
+                if (t >= lo && t < hi) atomicAdd(&L.cnt[rank_of(L, t - lo)], 1u);
+            });
+        if (c.ban_on) ngram_each<NT>(a, c, lo, hi, [&](uint32_t t) { atomicOr(&L.cnt[rank_of(L, t - lo)], CNT_BAN); });
+        __syncthreads();
+    }
+    return ranked;
+}
+
+// Every processor in order for one special id e with raw logit l, window count
+// cnt (CNT_BAN if banned) and mask word mw: repetition → presence/frequency →
+// bias → mask → n-gram ban (sampling.rs:857-920 for the first and last; the
+// others are this build's extensions).
+template <int NT, uint32_t SEGMAX>
+__device__ __forceinline__ float special_value(const RowCtx& c, const ProcLds<NT, SEGMAX>& L, uint32_t e,
+                                               float l, uint32_t cw, uint32_t mw) {
+    const uint32_t cnt = cw & ~CNT_BAN;
+    if (c.cnt_on && cnt) {
+        if (c.rep_on) {
+            const float rep = c.p.repetition_penalty;
+            l = l < 0.0f ? __fmul_rn(l, rep) : __fdiv_rn(l, rep);
+        }
+        if (c.pf_on) {
+            l = __fsub_rn(l, __fmul_rn(c.p.frequency_penalty, (float)cnt));
+            l = __fsub_rn(l, c.p.presence_penalty);
+        }
+    }
+    if (c.bias_on)
+        for (uint32_t j = 0; j < L.nbias; ++j)
+            if (L.bias_id[j] == e) l = __fadd_rn(l, L.bias_v[j]);
+    if (c.mask_on && !((mw >> (e & 31u)) & 1u)) l = -INFINITY;
+    if (cw & CNT_BAN) l = -INFINITY;
+    return l;
+}
+
+template <int DT>
+__device__ __forceinline__ float raw_at(const char* rp, uint32_t e) {
+    return DT == AXS_DTYPE_BF16 ? __uint_as_float((uint32_t)((const uint16_t*)rp)[e] << 16)
+                                : ((const float*)rp)[e];
+}
+
+// count word of an unranked special id, from HBM: window occurrences and the
+// n-gram ban (one scan each)
+__device__ __forceinline__ uint32_t count_word_hbm(const KArgs& a, const RowCtx& c, uint32_t e) {
+    uint32_t cnt = 0;
+    if (c.cnt_on)
+        for (int64_t i = c.w0; i < c.w1; ++i) cnt += a.hist[i] == e ? 1u : 0u;
     if (c.ban_on) {
-        // logits_with_no_repeat_ngram_in_place (sampling.rs:896-920)
-        int64_t nhist = c.w1 - c.h0;
-        uint32_t ng = c.p.no_repeat_ngram_size;
+        const int64_t nhist = c.w1 - c.h0;
+        const uint32_t ng = c.p.no_repeat_ngram_size;
         int64_t keep = (int64_t)(c.p.ngram_window > ng ? c.p.ngram_window : ng);
         if (keep > nhist) keep = nhist;
-        int64_t hs = c.w1 - keep;
-        int64_t plen = (int64_t)ng - 1;
-        for (int64_t s = tid; s + (int64_t)ng <= keep; s += NT_CHUNK) {
+        const int64_t hs = c.w1 - keep;
+        const int64_t plen = (int64_t)ng - 1;
+        for (int64_t s = 0; s + (int64_t)ng <= keep; ++s) {
+            if (a.hist[hs + s + plen] != e) continue;
             bool match = true;
             for (int64_t j = 0; j < plen; ++j)
                 if (a.hist[hs + s + j] != a.hist[c.w1 - plen + j]) {
@@ -377,54 +565,62 @@ __device__ __forceinline__ void proc_setup(const KArgs& a, const RowCtx& c, uint
                     break;
                 }
             if (match) {
-                uint32_t t = a.hist[hs + s + plen];
-                if (t >= lo && t < hi) atomicOr(&L.ban[(t - lo) >> 5], 1u << ((t - lo) & 31u));
-            }
-        }
-    }
-    __syncthreads();
-}
-
-// Processor flags of a row
-constexpr uint32_t PF_REP = 1u, PF_PF = 2u, PF_CNT = 4u, PF_BIAS = 8u;
-
-// Repetition → presence/frequency → bias for one id that carries a history
-// count or a bias entry (mask and n-gram ban are applied by the caller).
-__device__ __forceinline__ float proc_special(const uint32_t* __restrict__ hist, const ProcLds& L,
-                                              uint32_t off, uint32_t e, float l, uint32_t pfl,
-                                              float rep, float freq, float pres, int64_t w0,
-                                              int64_t w1) {
-    if (pfl & PF_CNT) {
-        // occurrences of e in the repetition window, from the LDS hash
-        const uint32_t key = off + 1u;
-        uint32_t h = hslot(off);
-        uint32_t cnt = 0;
-        bool found = false;
-        for (uint32_t probe = 0; probe < HSLOTS; ++probe) {
-            uint32_t k = L.hkey[h];
-            if (k == key) {
-                cnt = L.hval[h];
-                found = true;
+                cnt |= CNT_BAN;
                 break;
             }
-            if (k == 0u) break;
-            h = (h + 1u) & (HSLOTS - 1u);
-        }
-        if (!found && L.hfull) {  // the table overflowed: count in HBM
-            for (int64_t i = w0; i < w1; ++i) cnt += hist[i] == e ? 1u : 0u;
-        }
-        if (cnt) {
-            if (pfl & PF_REP) l = l < 0.0f ? __fmul_rn(l, rep) : __fdiv_rn(l, rep);
-            if (pfl & PF_PF) {
-                l = __fsub_rn(l, __fmul_rn(freq, (float)cnt));
-                l = __fsub_rn(l, pres);
-            }
         }
     }
-    if (pfl & PF_BIAS)
-        for (uint32_t j = 0; j < L.nbias; ++j)
-            if (L.bias_id[j] == e) l = __fadd_rn(l, L.bias_v[j]);
-    return l;
+    return cnt;
+}
+
+// f(e, processed logit) for the special ids of ranks rk0, rk0 + 1, ... (thread
+// t takes ranks rk0 + t + k*NT, eight at a time with every load issued before
+// any is used), or, for an unranked segment, for every special id by walking
+// the bitmap.
+template <int DT, int NT, uint32_t SEGMAX, typename F>
+__device__ __forceinline__ void visit_specials(const KArgs& a, const RowCtx& c, const ProcLds<NT, SEGMAX>& L,
+                                               bool ranked, uint32_t rk0, int r, const char* rp, uint32_t lo,
+                                               uint32_t hi, F&& f) {
+    using PL = ProcLds<NT, SEGMAX>;
+    const int tid = threadIdx.x;
+    if (ranked) {
+        const uint32_t n = L.nspec;
+        for (uint32_t b = rk0 + (uint32_t)tid; b < n; b += 8u * NT) {
+            float raw[8];
+            uint32_t mw[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t rk = b + (uint32_t)q * NT;
+                raw[q] = 0.0f;
+                mw[q] = 0xFFFFFFFFu;
+                if (rk < n) {
+                    const uint32_t e = L.sid[rk];
+                    raw[q] = raw_at<DT>(rp, e);
+                    if (c.mask_on) mw[q] = a.mask[(size_t)r * a.mask_stride + (e >> 5)];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                const uint32_t rk = b + (uint32_t)q * NT;
+                if (rk < n) {
+                    const uint32_t e = L.sid[rk];
+                    f(e, special_value(c, L, e, raw[q], L.cnt[rk], mw[q]));
+                }
+            }
+        }
+        return;
+    }
+    const uint32_t nw = (hi - lo + 31u) / 32u;
+    for (uint32_t wi = tid; wi < nw; wi += NT) {
+        uint32_t bits = L.spec[wi];
+        while (bits) {
+            const uint32_t b = (uint32_t)__ffs((int)bits) - 1u;
+            bits &= bits - 1u;
+            const uint32_t e = lo + wi * 32u + b;
+            const uint32_t mw = c.mask_on ? a.mask[(size_t)r * a.mask_stride + (e >> 5)] : 0xFFFFFFFFu;
+            f(e, special_value(c, L, e, raw_at<DT>(rp, e), count_word_hbm(a, c, e), mw));
+        }
+    }
 }
 
 // Segment geometry: thread t holds NV vectors of EPV consecutive ids; vector j
@@ -487,59 +683,28 @@ __device__ __forceinline__ float unpack(const u32x4& w, int q) {
     return __uint_as_float(w[q]);
 }
 
-// Visits every id of the segment once, with its processed logit: f(id, l).
-// Ids without a special bit come from the thread's registers (mask applied
-// inline); ids with a history count, a bias entry or an n-gram ban are
-// visited in a second loop over the segment's bitmaps, which re-reads their
-// raw logits (a few per segment) and applies every processor in order.
-template <int DT, int NV, typename F>
-__device__ __forceinline__ void seg_visit(const KArgs& a, const RowCtx& c, const ProcLds& L, int r,
-                                          uint32_t lo, uint32_t hi, Seg<DT, NV>& S, F&& f) {
+// Register part of a pass: f(id, l) for every id the thread holds.  Special
+// ids are skipped; they are visited by visit_specials.
+template <int DT, int NV, int NT, uint32_t SEGMAX, typename F>
+__device__ __forceinline__ void regs_visit(const RowCtx& c, const ProcLds<NT, SEGMAX>& L, uint32_t lo,
+                                           Seg<DT, NV>& S, bool special, F&& f) {
     constexpr int EPV = Ev<DT>::EPV;
     const int tid = threadIdx.x;
-    const uint32_t pfl = (c.rep_on ? PF_REP : 0u) | (c.pf_on ? PF_PF : 0u) |
-                         (c.cnt_on ? PF_CNT : 0u) | (c.bias_on ? PF_BIAS : 0u);
-    const bool special = pfl != 0u || c.ban_on;
 #pragma unroll
     for (int j = 0; j < NV; ++j) {
         // recompute from the raw registers in every pass (keeps the unpacked
         // values out of the register budget)
         asm volatile("" : "+v"(S.raw[j]));
-        const uint32_t e0 = lo + ((uint32_t)j * NT_CHUNK + tid) * EPV;
+        const uint32_t e0 = lo + ((uint32_t)j * NT + tid) * EPV;
         const uint32_t off0 = e0 - lo;
-        uint32_t skip = 0;
-        if (special)
-            skip = ((L.spec[off0 >> 5] | L.ban[off0 >> 5]) >> (off0 & 31u)) & ((1u << EPV) - 1u);
+        uint32_t sk = 0;
+        if (special) sk = (L.spec[off0 >> 5] >> (off0 & 31u)) & ((1u << EPV) - 1u);
 #pragma unroll
         for (int q = 0; q < EPV; ++q) {
-            if ((skip >> q) & 1u) continue;
             float l = unpack<DT>(S.raw[j], q);
             if (c.mask_on && !((S.mw[j] >> ((e0 + q) & 31u)) & 1u)) l = -INFINITY;
+            if ((sk >> q) & 1u) continue;
             f(e0 + q, l);
-        }
-    }
-    if (special) {
-        const char* rp = row_ptr(a, r);
-        const uint32_t nw = (hi - lo + 31u) / 32u;
-        for (uint32_t wi = tid; wi < nw; wi += NT_CHUNK) {
-            uint32_t bits = L.spec[wi] | L.ban[wi];
-            while (bits) {
-                const uint32_t b = (uint32_t)__ffs((int)bits) - 1u;
-                bits &= bits - 1u;
-                const uint32_t off = wi * 32u + b;
-                const uint32_t e = lo + off;
-                float l = DT == AXS_DTYPE_BF16 ? __uint_as_float((uint32_t)((const uint16_t*)rp)[e] << 16)
-                                               : ((const float*)rp)[e];
-                if ((L.spec[wi] >> b) & 1u)
-                    l = proc_special(a.hist, L, off, e, l, pfl, c.p.repetition_penalty,
-                                     c.p.frequency_penalty, c.p.presence_penalty, c.w0, c.w1);
-                if (c.mask_on) {
-                    uint32_t mw = a.mask[(size_t)r * a.mask_stride + (e >> 5)];
-                    if (!((mw >> (e & 31u)) & 1u)) l = -INFINITY;
-                }
-                if ((L.ban[wi] >> b) & 1u) l = -INFINITY;
-                f(e, l);
-            }
         }
     }
 }
@@ -553,159 +718,6 @@ __device__ __forceinline__ int64_t xcd_item(int64_t total) {
     return (b % 8) * per + b / 8;
 }
 
-// wave-aggregated append of a candidate into LDS (one LDS atomic per wave)
-__device__ __forceinline__ void cand_append(bool in, uint32_t id, float l, uint32_t* s_n, Cand* s_cand) {
-    const int lane = threadIdx.x & 63;
-    uint64_t m = __ballot(in);
-    if (m == 0ull) return;
-    uint32_t base = 0;
-    int leader = __ffsll((long long)m) - 1;
-    if (lane == leader) base = atomicAdd(s_n, (uint32_t)__popcll(m));
-    base = (uint32_t)__shfl((int)base, leader, 64);
-    if (in) {
-        uint32_t slot = base + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-        if (slot < CAPC) {
-            s_cand[slot].id = id;
-            s_cand[slot].l = l;
-        }
-    }
-}
-
-// --------------------------------------------------------------------------
-// k_chunk: the single pass over the logits, one segment per workgroup
-// --------------------------------------------------------------------------
-template <int DT, int NV>
-__global__ __launch_bounds__(NT_CHUNK) void k_chunk(KArgs a) {
-    __shared__ ProcLds L;
-    __shared__ Cand s_cand[CAPC];
-    __shared__ uint32_t s_hist[NBIN];
-    __shared__ float s_f[NT_CHUNK / 64];
-    __shared__ uint32_t s_u[NT_CHUNK / 64];
-    __shared__ uint32_t s_n;
-    __shared__ uint32_t s_bstar;
-
-    const int tid = threadIdx.x;
-    if (blockIdx.x == 0 && tid == 0) *a.exact_count = 0;
-    const int64_t total = (int64_t)a.nrows * a.nch;
-    const int64_t w = xcd_item(total);
-    if (w >= total) return;
-    const int r = (int)(w / a.nch);
-    const int ci = (int)(w % a.nch);
-    const uint32_t lo = (uint32_t)ci * (uint32_t)a.chunk;
-    const uint32_t hi = min(lo + (uint32_t)a.chunk, (uint32_t)a.vocab);
-
-    RowCtx c = make_ctx(a, r);
-    Seg<DT, NV> S;
-    seg_load<DT, NV>(a, r, lo, hi, a.vec != 0, c.mask_on, S);  // in flight during the setup
-    if (c.any_proc) proc_setup(a, c, lo, hi, L);
-
-    // max and first argmax (NaN skipped)
-    float bm = -INFINITY;
-    uint32_t bi = NONE;
-    seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
-        if (!isnan(l)) am_merge(bm, bi, l, e);
-    });
-    block_argmax<NT_CHUNK>(bm, bi, s_f, s_u);
-    const float mc = bi == NONE ? -INFINITY : bm;
-
-    ChunkStat st;
-    st.m = mc;
-    st.amax = bi;
-    st.lx = -INFINITY;
-    st.count = 0;
-    st.flags = (c.err || (c.any_proc && L.err)) ? CS_ERROR : 0u;
-    st.gsum = 0.0f;
-    st.pad0 = st.pad1 = 0;
-
-    const uint32_t mode = c.mode;
-    if (mode == M_GREEDY) {
-        if (a.want_logprob && isfinite(mc)) {
-            float s = 0.0f;
-            seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t, float l) {
-                if (isfinite(l)) s += __expf(l - mc);
-            });
-            st.gsum = block_sum_f<NT_CHUNK>(s, s_f);
-        }
-    } else if ((mode == M_MINP || mode == M_TOPK) && isfinite(mc)) {
-        const float inv = __fdiv_rn(1.0f, c.p.temperature);
-        if (isfinite(inv)) {
-            if (tid == 0) s_n = 0;
-            const bool use_bins = mode == M_TOPK;
-            uint32_t bstar = 0;
-            float thr = 0.0f;
-            if (use_bins) {
-                if (c.p.top_k > CAPC) {
-                    st.flags |= CS_OVERFLOW;
-                } else {
-                    for (uint32_t i = tid; i < NBIN; i += NT_CHUNK) s_hist[i] = 0;
-                    __syncthreads();
-                    seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t, float l) {
-                        float x = __fmul_rn(__fsub_rn(mc, l), inv);
-                        if (x < 64.0f) atomicAdd(&s_hist[(uint32_t)(x * 32.0f)], 1u);
-                    });
-                    __syncthreads();
-                    uint32_t loc = 0;
-#pragma unroll
-                    for (int q = 0; q < NBIN / NT_CHUNK; ++q) loc += s_hist[tid * (NBIN / NT_CHUNK) + q];
-                    uint32_t tot;
-                    uint32_t pre = block_excl_scan_u32<NT_CHUNK>(loc, s_u, &tot);
-                    const uint32_t K = c.p.top_k;
-                    if (tid == 0) {
-                        s_bstar = NBIN - 1;
-                        s_n = tot;  // gathered-set size when every binned id is taken
-                    }
-                    __syncthreads();
-                    if (tot >= K && pre < K && pre + loc >= K) {
-                        uint32_t acc = pre;
-                        for (int q = 0; q < NBIN / NT_CHUNK; ++q) {
-                            acc += s_hist[tid * (NBIN / NT_CHUNK) + q];
-                            if (acc >= K) {
-                                s_bstar = tid * (NBIN / NT_CHUNK) + q;
-                                s_n = acc;
-                                break;
-                            }
-                        }
-                    }
-                    __syncthreads();
-                    bstar = s_bstar;
-                    if (s_n > CAPC) st.flags |= CS_OVERFLOW;
-                    __syncthreads();
-                    if (tid == 0) s_n = 0;
-                }
-            } else {
-                thr = __fsub_rn(ln_f32(c.p.min_p), 1e-3f);
-            }
-            __syncthreads();
-            if (!(st.flags & CS_OVERFLOW)) {
-                float lx = -INFINITY;
-                seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
-                    bool in = false;
-                    if (!isnan(l)) {
-                        if (use_bins) {
-                            float x = __fmul_rn(__fsub_rn(mc, l), inv);
-                            in = x < 64.0f && (uint32_t)(x * 32.0f) <= bstar;
-                        } else {
-                            in = __fmul_rn(__fsub_rn(l, mc), inv) >= thr;
-                        }
-                        if (!in) lx = fmaxf(lx, l);
-                    }
-                    cand_append(in, e, l, &s_n, s_cand);
-                });
-                lx = block_max<NT_CHUNK>(lx, s_f);
-                uint32_t n = s_n;
-                if (n > CAPC) {
-                    st.flags |= CS_OVERFLOW;
-                } else {
-                    Cand* dst = a.cand + ((size_t)r * a.nch + ci) * CAPC;
-                    for (uint32_t i = tid; i < n; i += NT_CHUNK) dst[i] = s_cand[i];
-                    st.count = n;
-                    st.lx = lx;
-                }
-            }
-        }
-    }
-    if (tid == 0) a.cstat[(size_t)r * a.nch + ci] = st;
-}
 // --------------------------------------------------------------------------
 // outputs
 // --------------------------------------------------------------------------
@@ -734,42 +746,156 @@ __device__ __forceinline__ double ulp_f(float x) {
     return (double)nextafterf(ax, INFINITY) - (double)ax;
 }
 
-// --------------------------------------------------------------------------
-// k_finish: one workgroup per row
-// --------------------------------------------------------------------------
-__global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
-    __shared__ uint64_t s_key[FIN_CAP];
-    __shared__ float s_f[NT_FIN / 64];
-    __shared__ uint32_t s_u[NT_FIN / 64];
-    __shared__ double s_d[NT_FIN / 64];
-    __shared__ uint32_t s_n;
-    __shared__ float s_mg;
-    __shared__ uint32_t s_coff[MAX_SEGS + 1];
-    const int r = blockIdx.x;
-    const int tid = threadIdx.x;
-    if (r >= a.nrows) return;
-    const axs_sampling_params p = row_params(a, r);
-    const uint32_t mode = row_mode(p);
-    const int nch = a.nch;
+// lane k's value of v (k uniform)
+__device__ __forceinline__ float lane_f(float v, int k) {
+    return __uint_as_float((uint32_t)__builtin_amdgcn_readlane((int)__float_as_uint(v), k));
+}
 
-    float m = -INFINITY;
-    uint32_t am = NONE;
-    float lx = -INFINITY;
-    uint32_t fl = 0;
-    for (int c = tid; c < nch; c += NT_FIN) {
-        ChunkStat st = a.cstat[(size_t)r * nch + c];
-        am_merge(m, am, st.m, st.amax);
-        lx = fmaxf(lx, st.lx);
-        fl |= st.flags;
+// --------------------------------------------------------------------------
+// Row finish
+// --------------------------------------------------------------------------
+template <int NT>
+struct FinLds {
+    uint64_t key[FIN_CAP];
+    uint32_t cnt[MAX_SEGS];  // candidates published by each segment
+    float rf[NT / 64];
+    uint32_t ru[NT / 64];
+    double rd[NT / 64];
+    uint32_t n;
+};
+
+// Sequential decisions over n sorted candidates (F.key), the reference's own
+// f32 loops (sampling.rs:283-316, 922-952), run by wave 0: the candidates are
+// read 64 at a time, one per lane, and the running f32 sums walk them with
+// readlane so no step of the chain waits on LDS.
+template <int NT>
+__device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_sampling_params& p, uint32_t mode,
+                                              bool sorted, const FinLds<NT>& F, uint32_t n, uint32_t flags0) {
+    const int lane = threadIdx.x & 63;
+    auto P = [&](uint64_t k) { return sorted ? pdesc_p(k) : idasc_p(k); };
+    auto ID = [&](uint64_t k) { return sorted ? pdesc_id(k) : idasc_id(k); };
+    uint32_t flags = flags0 | AXS_FLAG_DREW;
+    const uint32_t L = n;
+    uint32_t nk = L;
+    if (sorted && topp_active(p)) {
+        // top-p over the full candidate mass (sampling.rs:931-945)
+        float total = 0.0f;
+        for (uint32_t b = 0; b < L; b += 64) {
+            const uint32_t i = b + lane;
+            const float pv = i < L ? P(F.key[i]) : 0.0f;
+            const uint32_t cnt = min(64u, L - b);
+            for (uint32_t k = 0; k < cnt; ++k) total = __fadd_rn(total, lane_f(pv, (int)k));
+        }
+        const float cutoff = __fmul_rn(p.top_p, total);
+        float cum = 0.0f, prev = 0.0f;
+        uint32_t keep = 0;
+        bool done = false;
+        for (uint32_t b = 0; b < L && !done; b += 64) {
+            const uint32_t i = b + lane;
+            const float pv = i < L ? P(F.key[i]) : 0.0f;
+            const uint32_t cnt = min(64u, L - b);
+            for (uint32_t k = 0; k < cnt; ++k) {
+                prev = cum;
+                cum = __fadd_rn(cum, lane_f(pv, (int)k));
+                keep += 1;
+                if (cum >= cutoff) {
+                    done = true;
+                    break;
+                }
+            }
+        }
+        nk = keep > 1 ? keep : 1;
+        const double up = (double)cum - (double)cutoff;
+        const double lo = keep > 1 ? (double)cutoff - (double)prev : INFINITY;
+        if (fmin(up, lo) / (double)total < 1e-6 && (p.top_k == 0 || nk <= p.top_k))
+            flags |= AXS_FLAG_NEAR_NUCLEUS;
     }
-    block_argmax<NT_FIN>(m, am, s_f, s_u);
-    lx = block_max<NT_FIN>(lx, s_f);
-    fl = block_or_u32<NT_FIN>(fl, s_u);
+    uint32_t kept = nk;
+    if (sorted && p.top_k > 0 && kept > p.top_k) kept = p.top_k;
+    if (sorted && kept < L) {
+        const float pa = P(F.key[kept - 1]);
+        const float pb = P(F.key[kept]);
+        // near but not identical probabilities across the cut (identical ones
+        // come from equal logits and are ordered by id everywhere)
+        if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
+    }
+    float Fs = 0.0f;
+    for (uint32_t b = 0; b < kept; b += 64) {
+        const uint32_t i = b + lane;
+        const float pv = i < kept ? P(F.key[i]) : 0.0f;
+        const uint32_t cnt = min(64u, kept - b);
+        for (uint32_t k = 0; k < cnt; ++k) Fs = __fadd_rn(Fs, lane_f(pv, (int)k));
+    }
+    const float u = row_uniform(a, r, p);
+    const float thr = __fmul_rn(u, Fs);
+    float cum = 0.0f, prev = 0.0f;
+    uint32_t j = kept;
+    for (uint32_t b = 0; b < kept && j == kept; b += 64) {
+        const uint32_t i = b + lane;
+        const float pv = i < kept ? P(F.key[i]) : 0.0f;
+        const uint32_t cnt = min(64u, kept - b);
+        for (uint32_t k = 0; k < cnt; ++k) {
+            prev = cum;
+            cum = __fadd_rn(cum, lane_f(pv, (int)k));
+            if (cum >= thr) {
+                j = b + k;
+                break;
+            }
+        }
+    }
+    if (j == kept) {
+        // last maximum (sampling.rs:310-315); unreachable for u <= 1
+        float bp = -1.0f;
+        for (uint32_t i = 0; i < kept; ++i)
+            if (P(F.key[i]) >= bp) {
+                bp = P(F.key[i]);
+                j = i;
+            }
+    } else {
+        const double up = (double)cum - (double)thr;
+        const double lo = j > 0 ? (double)thr - (double)prev : INFINITY;
+        if (fmin(up, lo) / (double)Fs < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
+    }
+    if (lane == 0) {
+        const float pj = P(F.key[j]);
+        write_row(a, r, ID(F.key[j]), logprob_of(__fdiv_rn(pj, Fs)), flags);
+        if (a.out_kept_count) a.out_kept_count[r] = kept;
+        if (a.ws_kept_id) {
+            a.rstate[r].kept = kept;
+            a.rstate[r].nlist = kept < KEPT_CAP ? kept : KEPT_CAP;
+            a.rstate[r].F = Fs;
+            a.rstate[r].flags = flags;
+        }
+    }
+    if (a.out_kept && a.out_kept_cap > 0) {
+        const uint32_t nw = kept < (uint32_t)a.out_kept_cap ? kept : (uint32_t)a.out_kept_cap;
+        for (uint32_t i = lane; i < nw; i += 64) a.out_kept[(size_t)r * a.out_kept_cap + i] = ID(F.key[i]);
+    }
+    if (a.ws_kept_id) {
+        const uint32_t nw = kept < KEPT_CAP ? kept : KEPT_CAP;
+        for (uint32_t i = lane; i < nw; i += 64) {
+            a.ws_kept_id[(size_t)r * KEPT_CAP + i] = ID(F.key[i]);
+            a.ws_kept_p[(size_t)r * KEPT_CAP + i] = P(F.key[i]);
+        }
+    }
+}
+
+// The row's decision from its merged statistics: the maximum m and its lowest
+// id am (NONE for an all-NaN row), the CS_* flags, gs = the sum of exp(l - m)
+// over finite l (greedy logprob), and cands(f), which calls f(id, l) for this
+// thread's share of the ncand gathered candidates (a superset of the ids that
+// survive min-p).  Rows it cannot decide are listed for the exact path.
+// Called by all threads of the workgroup (uniform control flow).
+template <int NT, typename CF>
+__device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_sampling_params& p, float m,
+                                              uint32_t am, uint32_t fl, double gs, uint32_t ncand,
+                                              FinLds<NT>& F, CF&& cands) {
+    const int tid = threadIdx.x;
+    const uint32_t mode = row_mode(p);
     if (am == NONE) {  // all-NaN row: argmax_f32 → 0 (sampling.rs:966)
         am = 0;
         m = -INFINITY;
     }
-
     if (fl & CS_ERROR) {
         if (tid == 0) {
             write_row(a, r, 0u, NAN, AXS_FLAG_ERROR);
@@ -782,26 +908,15 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
         }
         return;
     }
-
     if (mode == M_GREEDY) {
-        float lp = NAN;
-        if (a.want_logprob) {
-            double gs = 0.0;
-            for (int c = tid; c < nch; c += NT_FIN) {
-                ChunkStat st = a.cstat[(size_t)r * nch + c];
-                if (isfinite(st.m) && st.amax != NONE) gs += (double)st.gsum * exp((double)st.m - (double)m);
-            }
-            gs = block_sum_d<NT_FIN>(gs, s_d);
-            if (isfinite(m) && gs > 0.0) lp = (float)(-log(gs));
-        }
         if (tid == 0) {
+            const float lp = (a.want_logprob && isfinite(m) && gs > 0.0) ? (float)(-log(gs)) : NAN;
             write_row(a, r, am, lp, AXS_FLAG_GREEDY);
             write_single_kept(a, r, am);
             if (a.ws_kept_id) a.rstate[r].flags = AXS_FLAG_GREEDY;
         }
         return;
     }
-
     const float inv = __fdiv_rn(1.0f, p.temperature);
     if (!(isfinite(m) && isfinite(inv))) {
         // every probability is zero or NaN → argmax (sampling.rs:264-266,279-281)
@@ -812,169 +927,53 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
         }
         return;
     }
-
     const bool minp = mode == M_MINP;
     const bool sorted = minp ? filters_enabled(p) : (mode != M_FAST);
-    bool exact = !(mode == M_MINP || mode == M_TOPK) || (fl & CS_OVERFLOW);
-
-    // candidate merge: every gathered id above the global exclusion level lx
-    float plx = -1.0f;
+    bool exact = !minp || (fl & CS_OVERFLOW) || ncand > FIN_CAP;
     if (!exact) {
-        if (tid == 0) {
-            s_n = 0;
-            s_mg = INFINITY;
-        }
+        // min-p survivors: p = exp((l - m) / T) >= min_p (cutoff = min_p *
+        // max_prob, max_prob = 1)
+        if (tid == 0) F.n = 0;
         __syncthreads();
         float mg = INFINITY;
-        // candidate counts of every segment → prefix offsets, then one flat
-        // parallel loop over all candidates of the row
-        uint32_t loc = 0;
-        constexpr uint32_t PER = MAX_SEGS / NT_FIN;
-        for (uint32_t q = 0; q < PER; ++q) {
-            uint32_t c = (uint32_t)tid * PER + q;
-            uint32_t cnt = c < (uint32_t)nch ? a.cstat[(size_t)r * nch + c].count : 0u;
-            s_coff[c] = cnt;
-            loc += cnt;
-        }
-        uint32_t ntot;
-        uint32_t pre = block_excl_scan_u32<NT_FIN>(loc, s_u, &ntot);
-        for (uint32_t q = 0; q < PER; ++q) {
-            uint32_t c = (uint32_t)tid * PER + q;
-            uint32_t cnt = s_coff[c];
-            s_coff[c] = pre;
-            pre += cnt;
-        }
-        if (tid == 0) s_coff[MAX_SEGS] = ntot;
-        __syncthreads();
-        for (uint32_t i = tid; i < ntot; i += NT_FIN) {
-            uint32_t lo_c = 0, hi_c = (uint32_t)nch;  // last c with s_coff[c] <= i
-            while (hi_c - lo_c > 1) {
-                uint32_t mid = (lo_c + hi_c) / 2;
-                if (s_coff[mid] <= i) lo_c = mid;
-                else hi_c = mid;
-            }
-            {
-                const uint32_t c = lo_c;
-                Cand cd = a.cand[((size_t)r * nch + c) * CAPC + (i - s_coff[c])];
-                if (!(cd.l > lx)) continue;
-                float pr = prob_of(cd.l, m, inv);
-                uint64_t key;
-                if (minp) {
-                    float d = fabsf(pr - p.min_p) / p.min_p;
-                    mg = fminf(mg, d);
-                    if (!(pr >= p.min_p)) continue;  // cutoff = min_p * max_prob, max_prob = 1
-                    key = sorted ? key_pdesc(pr, cd.id) : key_idasc(pr, cd.id);
-                } else {
-                    key = key_pdesc(pr, cd.id);
-                }
-                uint32_t slot = atomicAdd(&s_n, 1u);
-                if (slot < FIN_CAP) s_key[slot] = key;
-            }
-        }
-        mg = block_max<NT_FIN>(-mg, s_f);  // min via max of negatives
-        if (tid == 0) s_mg = -mg;
-        __syncthreads();
-        uint32_t n = s_n;
-        if (lx > -INFINITY) plx = prob_of(lx, m, inv);
-        if (n > FIN_CAP || n == 0) exact = true;
-        // min-p: complete iff every id left out has p < min_p
-        if (minp && plx >= p.min_p) exact = true;
+        cands([&](uint32_t id, float l) {
+            const float pr = prob_of(l, m, inv);
+            mg = fminf(mg, fabsf(pr - p.min_p) / p.min_p);
+            if (!(pr >= p.min_p)) return;
+            const uint32_t slot = atomicAdd(&F.n, 1u);
+            F.key[slot] = sorted ? key_pdesc(pr, id) : key_idasc(pr, id);
+        });
+        mg = -block_max<NT>(-mg, F.rf);
+        const uint32_t n = F.n;
+        if (n == 0) exact = true;  // (unreachable: the maximum itself has p = 1)
         if (!exact) {
-            uint32_t np2 = next_pow2(n);
-            for (uint32_t i = n + tid; i < np2; i += NT_FIN) s_key[i] = 0;
-            __syncthreads();
-            block_sort_desc<NT_FIN>(s_key, np2);
-            if (mode == M_TOPK) {
-                uint32_t K = p.top_k < (uint32_t)a.vocab ? p.top_k : (uint32_t)a.vocab;
-                if (n < K) exact = true;
-                else {
-                    float pk = pdesc_p(s_key[K - 1]);
-                    if (!(pk > plx) || !(pk > 0.0f)) exact = true;
+            const uint32_t flags0 = mg < 1e-6f ? AXS_FLAG_NEAR_MINP : 0u;
+            if (n <= 64) {
+                if (tid < 64) {
+                    uint64_t k = (uint32_t)tid < n ? F.key[tid] : 0ull;
+                    k = wave_sort_desc(k);
+                    F.key[tid] = k;
                 }
-            }
-        }
-        if (!exact && tid == 0) {
-            // sequential decisions over the sorted candidates — the reference's
-            // own f32 loops (sampling.rs:283-316, 922-952)
-            const uint32_t L = n;
-            uint32_t flags = AXS_FLAG_DREW;
-            if (minp && s_mg < 1e-6f) flags |= AXS_FLAG_NEAR_MINP;
-            auto P = [&](uint32_t i) { return sorted ? pdesc_p(s_key[i]) : idasc_p(s_key[i]); };
-            auto ID = [&](uint32_t i) { return sorted ? pdesc_id(s_key[i]) : idasc_id(s_key[i]); };
-            uint32_t nk = L;
-            if (sorted && topp_active(p)) {
-                float total = 0.0f;
-                for (uint32_t i = 0; i < L; ++i) total = __fadd_rn(total, P(i));
-                float cutoff = __fmul_rn(p.top_p, total);
-                float cum = 0.0f, prev = 0.0f;
-                uint32_t keep = 0;
-                for (uint32_t i = 0; i < L; ++i) {
-                    prev = cum;
-                    cum = __fadd_rn(cum, P(i));
-                    keep += 1;
-                    if (cum >= cutoff) break;
-                }
-                nk = keep > 1 ? keep : 1;
-                double up = (double)cum - (double)cutoff;
-                double lo = keep > 1 ? (double)cutoff - (double)prev : INFINITY;
-                double mgn = fmin(up, lo) / (double)total;
-                if (mgn < 1e-6 && (p.top_k == 0 || nk <= p.top_k)) flags |= AXS_FLAG_NEAR_NUCLEUS;
-            }
-            uint32_t kept = nk;
-            if (sorted && p.top_k > 0 && kept > p.top_k) kept = p.top_k;
-            if (sorted && (kept < L || mode == M_TOPK)) {
-                float nextp = kept < L ? P(kept) : -1.0f;
-                if (mode == M_TOPK) nextp = fmaxf(nextp, plx);
-                // near but not identical probabilities across the cut (identical
-                // ones come from equal logits and are ordered by id everywhere)
-                if (nextp >= 0.0f && P(kept - 1) != nextp &&
-                    (double)P(kept - 1) - (double)nextp <= 2.0 * ulp_f(P(kept - 1)))
-                    flags |= AXS_FLAG_NEAR_TIE;
-            }
-            float F = 0.0f;
-            for (uint32_t i = 0; i < kept; ++i) F = __fadd_rn(F, P(i));
-            const float u = row_uniform(a, r, p);
-            const float thr = __fmul_rn(u, F);
-            float cum = 0.0f, prev = 0.0f;
-            uint32_t j = kept;
-            for (uint32_t i = 0; i < kept; ++i) {
-                prev = cum;
-                cum = __fadd_rn(cum, P(i));
-                if (cum >= thr) {
-                    j = i;
-                    break;
-                }
-            }
-            if (j == kept) {  // last maximum (sampling.rs:310-315)
-                float bp = -1.0f;
-                for (uint32_t i = 0; i < kept; ++i)
-                    if (P(i) >= bp) {
-                        bp = P(i);
-                        j = i;
+            } else if (n <= 256) {
+                if (tid < 64) {
+                    uint64_t k[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) {
+                        const uint32_t i = (uint32_t)(j * 64 + tid);
+                        k[j] = i < n ? F.key[i] : 0ull;
                     }
-            } else {
-                double up = (double)cum - (double)thr;
-                double lo = j > 0 ? (double)thr - (double)prev : INFINITY;
-                if (fmin(up, lo) / (double)F < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
-            }
-            const uint32_t tok = ID(j);
-            write_row(a, r, tok, logprob_of(__fdiv_rn(P(j), F)), flags);
-            if (a.out_kept) {
-                uint32_t nw = kept < (uint32_t)a.out_kept_cap ? kept : (uint32_t)a.out_kept_cap;
-                for (uint32_t i = 0; i < nw; ++i) a.out_kept[(size_t)r * a.out_kept_cap + i] = ID(i);
-            }
-            if (a.out_kept_count) a.out_kept_count[r] = kept;
-            if (a.ws_kept_id) {
-                uint32_t nw = kept < KEPT_CAP ? kept : KEPT_CAP;
-                for (uint32_t i = 0; i < nw; ++i) {
-                    a.ws_kept_id[(size_t)r * KEPT_CAP + i] = ID(i);
-                    a.ws_kept_p[(size_t)r * KEPT_CAP + i] = P(i);
+                    wave_sort_desc4(k);
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) F.key[j * 64 + tid] = k[j];
                 }
-                a.rstate[r].kept = kept;
-                a.rstate[r].nlist = nw;
-                a.rstate[r].F = F;
-                a.rstate[r].flags = flags;
+            } else {
+                const uint32_t np2 = next_pow2(n);
+                for (uint32_t i = n + tid; i < np2; i += NT) F.key[i] = 0ull;
+                __syncthreads();
+                block_sort_desc<NT>(F.key, np2);
             }
+            __syncthreads();
+            if (tid < 64) decide_sorted<NT>(a, r, p, mode, sorted, F, n, flags0);
         }
     }
     if (exact && tid == 0) {
@@ -994,9 +993,495 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
         rs.nlist = 0;
         rs.pad[0] = rs.pad[1] = rs.pad[2] = 0;
         a.rstate[r] = rs;
-        uint32_t idx = atomicAdd(a.exact_count, 1u);
+        const uint32_t idx = atomicAdd(a.exact_count, 1u);
         a.exact_rows[idx] = (uint32_t)r;
     }
+}
+
+// Merges the published results of the nseg segments of row r and decides it.
+template <int NT>
+__device__ __forceinline__ void finish_row(const KArgs& a, int r, int nseg, FinLds<NT>& F) {
+    const int tid = threadIdx.x;
+    float m = -INFINITY;
+    uint32_t am = NONE;
+    uint32_t fl = 0, ntot = 0;
+    for (int c = tid; c < nseg; c += NT) {
+        const ChunkStat st = sub_stat(&a.cstat[(size_t)r * nseg + c]);
+        am_merge(m, am, st.m, st.amax);
+        fl |= st.flags & 0xFFu;
+        F.cnt[c] = st.flags >> 8;
+        ntot += st.flags >> 8;
+    }
+    block_argmax<NT>(m, am, F.rf, F.ru);
+    fl = block_or_u32<NT>(fl, F.ru);
+    ntot = block_sum_u32<NT>(ntot, F.ru);
+    double gs = 0.0;
+    if (a.want_logprob) {
+        for (int c = tid; c < nseg; c += NT) {
+            const ChunkStat st = sub_stat(&a.cstat[(size_t)r * nseg + c]);
+            if (isfinite(st.m) && st.amax != NONE) gs += (double)st.gsum * exp((double)st.m - (double)m);
+        }
+        gs = block_sum_d<NT>(gs, F.rd);
+    }
+    const Cand* pool = a.pool + (size_t)r * nseg * CAPS;
+    finish_decide<NT>(a, r, row_params(a, r), m, am, fl, gs, ntot, F, [&](auto&& f) {
+        for (uint32_t i = tid; i < (uint32_t)nseg * CAPS; i += NT) {
+            if (i % CAPS >= F.cnt[i / CAPS]) continue;
+            const Cand cd = sub_cand(&pool[i]);
+            f(cd.id, cd.l);
+        }
+    });
+}
+
+// --------------------------------------------------------------------------
+// k_stream: the single pass over the logits.  One workgroup of NT threads per
+// (row, segment); with one segment per row (large batches) the workgroup owns
+// the whole row.  It builds the special-id bitmap of its segment from the
+// history while its first tiles load, then streams the segment in
+// double-buffered register tiles and keeps
+//   - the argmax of the processed logits (special ids resolved one by one),
+//   - min-p rows: every id within the min-p window of a lower bound of the
+//     row maximum (so nothing that survives min-p is missed),
+//   - greedy rows that want a logprob: the online sum of exp(l - max).
+// A one-segment row is decided in place.  Otherwise each workgroup publishes
+// its segment's result and the last one of the row to arrive (atomic arrival
+// counter, no waiting) merges and decides.
+// --------------------------------------------------------------------------
+template <int DT, int TV, bool MASK>
+struct Tile {
+    u32x4 raw[TV];
+    uint32_t mw[MASK ? TV : 1];
+};
+
+template <int DT, int TV, bool MASK, int NT>
+__device__ __forceinline__ void tile_load(const KArgs& a, int r, const char* rp, uint32_t t0, uint32_t hi,
+                                          Tile<DT, TV, MASK>& T) {
+    constexpr int EPV = Ev<DT>::EPV;
+    constexpr uint32_t TILE = (uint32_t)NT * TV * EPV;
+    const int tid = threadIdx.x;
+    if (a.vec && t0 + TILE <= hi) {
+        // whole tile in range (uniform): 16-byte nontemporal loads only
+#pragma unroll
+        for (int j = 0; j < TV; ++j) {
+            const uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+            T.raw[j] = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)e0 * (EPV == 8 ? 2 : 4)));
+            if (MASK) T.mw[j] = a.mask[(size_t)r * a.mask_stride + (e0 >> 5)];
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < TV; ++j) {
+        const uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+        if (a.vec && e0 + EPV <= hi) {
+            T.raw[j] = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)e0 * (EPV == 8 ? 2 : 4)));
+        } else {
+            uint32_t w[4];
+            if (DT == AXS_DTYPE_BF16) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t ea = e0 + 2 * q, eb = ea + 1;
+                    const uint32_t lo16 = ea < hi ? ((const uint16_t*)rp)[ea] : 0x7FC0u;
+                    const uint32_t hi16 = eb < hi ? ((const uint16_t*)rp)[eb] : 0x7FC0u;
+                    w[q] = lo16 | (hi16 << 16);
+                }
+            } else {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t ea = e0 + q;
+                    w[q] = ea < hi ? ((const uint32_t*)rp)[ea] : 0x7FC00000u;
+                }
+            }
+            T.raw[j] = u32x4{w[0], w[1], w[2], w[3]};
+        }
+        if (MASK) T.mw[j] = e0 < hi ? a.mask[(size_t)r * a.mask_stride + (e0 >> 5)] : 0u;
+    }
+}
+
+// Whole-vector tiles (16-byte aligned rows, segment end a multiple of EPV):
+// every lane loads, the lanes past the end re-read the tile's first vector
+// (their values are discarded by index), so the loads are the same on every
+// path and the compiler can keep the next tile in flight.
+template <int DT, int TV, bool MASK, int NT>
+__device__ __forceinline__ void tile_load_fast(const KArgs& a, int r, const char* rp, uint32_t t0, uint32_t hi,
+                                               Tile<DT, TV, MASK>& T) {
+    constexpr int EPV = Ev<DT>::EPV;
+    const int tid = threadIdx.x;
+#pragma unroll
+    for (int j = 0; j < TV; ++j) {
+        uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+        e0 = e0 < hi ? e0 : t0;
+        T.raw[j] = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)e0 * (EPV == 8 ? 2 : 4)));
+        if (MASK) T.mw[j] = a.mask[(size_t)r * a.mask_stride + (e0 >> 5)];
+    }
+}
+
+template <int NT, uint32_t SEGMAX>
+struct StreamLds {
+    static constexpr uint32_t CAPC = NT >= 1024 ? 2048u : 1024u;  // gathered candidates
+    union {
+        ProcLds<NT, SEGMAX> P;
+        FinLds<NT> F;
+    } u;
+    Cand cand[CAPC];
+    float red[NT / 64];
+    float redf[NT / 64];
+    uint32_t redu[NT / 64];
+    uint32_t ncand;
+    uint32_t last;
+};
+
+template <int DT, int TV, bool MASK, int NT, uint32_t SEGMAX>
+__global__ __launch_bounds__(NT) void k_stream(KArgs a) {
+    using SLT = StreamLds<NT, SEGMAX>;
+    constexpr int EPV = Ev<DT>::EPV;
+    constexpr uint32_t TILE = (uint32_t)NT * TV * EPV;
+    constexpr uint32_t CAPC = SLT::CAPC;
+    constexpr int CPT = (int)(CAPC / NT);  // candidates per thread
+    __shared__ SLT SL;
+    ProcLds<NT, SEGMAX>& L = SL.u.P;
+    const int tid = threadIdx.x;
+    const int wv = tid >> 6, lane = tid & 63;
+    const int nseg = a.snch;
+    const int64_t total = (int64_t)a.nrows * nseg;
+    const int64_t w = xcd_item(total);
+    if (w >= total) return;
+    const int r = (int)(w / nseg);
+    const int si = (int)(w % nseg);
+    const uint32_t lo = (uint32_t)si * (uint32_t)a.schunk;
+    const uint32_t hi = min(lo + (uint32_t)a.schunk, (uint32_t)a.vocab);
+    const uint32_t ntile = (hi - lo + TILE - 1) / TILE;
+    const char* rp = row_ptr(a, r);
+    // The workgroups start their segments at different tiles (the order of
+    // visits does not matter: ties are broken by id), so that they do not
+    // all read the same HBM channels at the same time.
+    const uint32_t rot = (uint32_t)(((uint64_t)w * 5u) % ntile);
+    auto tbase = [&](uint32_t k) {
+        uint32_t t = k + rot;
+        if (t >= ntile) t -= ntile;
+        return lo + t * TILE;
+    };
+
+    // loads in flight before anything waits: the segment's first two tiles,
+    // then the first round of the repetition window
+    const bool fast = a.vec && (hi % EPV) == 0;
+    Tile<DT, TV, MASK> b0, b1;
+    if (fast) {
+        tile_load_fast<DT, TV, MASK, NT>(a, r, rp, tbase(0), hi, b0);
+        if (ntile > 1) tile_load_fast<DT, TV, MASK, NT>(a, r, rp, tbase(1), hi, b1);
+    } else {
+        tile_load<DT, TV, MASK, NT>(a, r, rp, tbase(0), hi, b0);
+        if (ntile > 1) tile_load<DT, TV, MASK, NT>(a, r, rp, tbase(1), hi, b1);
+    }
+    const RowCtx c = make_ctx(a, r);
+    HistPre<NT> hp;
+    hist_prefetch<NT>(a, c, hp);
+    const bool special = c.cnt_on || c.bias_on || c.ban_on;
+    if (c.any_proc) proc_build<NT, SEGMAX>(a, c, lo, hi, L, hp);
+    bool ranked = true;
+    if (special) ranked = proc_rank<NT, SEGMAX>(a, c, lo, hi, L, hp);
+    // the first SPK*NT special ids' raw logits and mask words: loaded now,
+    // used after the stream, so the loads never hold up a tile
+    constexpr int SPK = 4;
+    // (kept as the loaded bits: converting them here would wait for the loads)
+    const uint32_t nspec = (special && ranked) ? L.nspec : 0u;
+    uint32_t sraw[SPK];
+    uint32_t smw[SPK];
+#pragma unroll
+    for (int k = 0; k < SPK; ++k) {
+        // unconditional loads (rank 0's id stands in past the end), so no
+        // branch merges a value that would have to be waited for here
+        const uint32_t rk = (uint32_t)tid + (uint32_t)k * NT;
+        const uint32_t e = rk < nspec ? L.sid[rk] : lo;
+        sraw[k] = DT == AXS_DTYPE_BF16 ? (uint32_t)((const uint16_t*)rp)[e] : ((const uint32_t*)rp)[e];
+        smw[k] = MASK ? a.mask[(size_t)r * a.mask_stride + (e >> 5)] : 0xFFFFFFFFu;
+    }
+    if (tid == 0) SL.ncand = 0;
+
+    const uint32_t mode = c.mode;
+    const float inv = __fdiv_rn(1.0f, c.p.temperature);
+    const bool gather = mode == M_MINP && isfinite(inv);
+    const bool gsum_on = mode == M_GREEDY && a.want_logprob;
+    const float thr = gather ? __fsub_rn(ln_f32(c.p.min_p), 1e-3f) : 0.0f;
+    const uint32_t sflags = (c.err || (c.any_proc && L.err)) ? CS_ERROR : 0u;
+
+    float tm = -INFINITY;             // thread maximum (non-special ids)
+    uint32_t ta = NONE;               // its lowest id
+    float gm = -INFINITY, gs = 0.0f;  // greedy logprob: sum of exp(l - gm)
+    float mrun = -INFINITY;           // a lower bound of the row maximum (wave-uniform)
+    float lpre = INFINITY;            // l < lpre ⇒ not a candidate (wave-uniform)
+
+    auto set_pre = [&]() {
+        // (l - mrun) * inv >= thr needs l >= mrun + thr / inv; the bound is
+        // lowered by 0.01 nats and a few ulps so rounding never excludes one
+        if (!isfinite(mrun)) {
+            lpre = INFINITY;
+        } else if (inv > 0.0f) {
+            const double bnd = (double)mrun + ((double)thr - 0.01) / (double)inv;
+            const double slack = 4.0 * fmax(fabs((double)mrun), fabs(bnd)) * 1.2e-7;
+            lpre = (float)(bnd - slack);
+        } else {
+            lpre = -INFINITY;
+        }
+    };
+    auto add_cand = [&](uint32_t e, float l) {
+        const uint32_t slot = atomicAdd(&SL.ncand, 1u);
+        if (slot < CAPC) {
+            SL.cand[slot].id = e;
+            SL.cand[slot].l = l;
+        }
+    };
+    auto gsum_add = [&](float l) {
+        if (isfinite(l)) {
+            if (l > gm) {
+                gs = __fmaf_rn(gs, __expf(gm - l), 1.0f);
+                gm = l;
+            } else {
+                gs += __expf(l - gm);
+            }
+        }
+    };
+    // the EPV logits of a vector as the processors see them, with the special
+    // ids as NaN: never a maximum, never gathered
+    auto vec_vals = [&](const u32x4& raw, uint32_t mw, uint32_t e0, float* v) {
+#pragma unroll
+        for (int q = 0; q < EPV; ++q) v[q] = unpack<DT>(raw, q);
+        if (MASK) {
+            const uint32_t mb = mw >> (e0 & 31u);
+#pragma unroll
+            for (int q = 0; q < EPV; ++q)
+                if (!((mb >> q) & 1u)) v[q] = -INFINITY;
+        }
+        if (special) {
+            const uint32_t off0 = e0 - lo;
+            const uint32_t sk = L.spec[off0 >> 5] >> (off0 & 31u);
+#pragma unroll
+            for (int q = 0; q < EPV; ++q)
+                if ((sk >> q) & 1u) v[q] = __builtin_nanf("");
+        }
+    };
+    // Per vector: its maximum decides everything.  The thread keeps the
+    // lowest-id vector holding its running maximum; the element is resolved
+    // once at the end.  Only vectors reaching the gather bound, and greedy
+    // rows that want a logprob, look at single elements.
+    uint32_t tj = NONE;  // first id of the best vector
+    u32x4 traw = u32x4{0u, 0u, 0u, 0u};
+    uint32_t tmw = 0xFFFFFFFFu;
+    auto process = [&](Tile<DT, TV, MASK>& T, uint32_t t0) {
+#pragma unroll
+        for (int j = 0; j < TV; ++j) {
+            asm volatile("" : "+v"(T.raw[j]));
+            const uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+            const uint32_t mw = MASK ? T.mw[j] : 0xFFFFFFFFu;
+            float v[EPV];
+            vec_vals(T.raw[j], mw, e0, v);
+            float vm = v[0];
+#pragma unroll
+            for (int q = 1; q < EPV; ++q) vm = fmaxf(vm, v[q]);
+            if (e0 >= hi) vm = __builtin_nanf("");  // a lane past the segment end
+            if (vm > tm || (vm == tm && e0 < tj)) {
+                tm = vm;
+                tj = e0;
+                traw = T.raw[j];
+                tmw = mw;
+            }
+            if (gather && vm >= lpre) {
+                // one slot reservation for all of the vector's candidates
+                uint32_t qm = 0;
+#pragma unroll
+                for (int q = 0; q < EPV; ++q)
+                    if (v[q] >= lpre && __fmul_rn(__fsub_rn(v[q], mrun), inv) >= thr) qm |= 1u << q;
+                if (qm) {
+                    uint32_t slot = atomicAdd(&SL.ncand, (uint32_t)__popc(qm));
+#pragma unroll
+                    for (int q = 0; q < EPV; ++q)
+                        if ((qm >> q) & 1u) {
+                            if (slot < CAPC) {
+                                SL.cand[slot].id = e0 + q;
+                                SL.cand[slot].l = v[q];
+                            }
+                            ++slot;
+                        }
+                }
+            }
+            if (gsum_on && e0 < hi) {
+#pragma unroll
+                for (int q = 0; q < EPV; ++q) gsum_add(v[q]);
+            }
+        }
+    };
+    // maximum of a tile (seeds the gather bound)
+    auto tile_max = [&](Tile<DT, TV, MASK>& T, uint32_t t0) {
+        float pm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < TV; ++j) {
+            const uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+            float v[EPV];
+            vec_vals(T.raw[j], MASK ? T.mw[j] : 0xFFFFFFFFu, e0, v);
+            if (e0 < hi)
+#pragma unroll
+                for (int q = 0; q < EPV; ++q) pm = fmaxf(pm, v[q]);
+        }
+        return pm;
+    };
+    // raises the wave's bound with its running maximum (no barrier)
+    auto raise = [&]() {
+        mrun = fmaxf(mrun, wave_max(tm));
+        set_pre();
+    };
+
+    if (gather) {
+        // the first tile's block maximum: one barrier, then waves go alone
+        const float v = wave_max(tile_max(b0, tbase(0)));
+        if (lane == 0) SL.red[wv] = v;
+        __syncthreads();
+        float mm = SL.red[0];
+#pragma unroll
+        for (int k = 1; k < NT / 64; ++k) mm = fmaxf(mm, SL.red[k]);
+        mrun = mm;
+        set_pre();
+    }
+    // tile t of the (rotated) order: seed the bound if the wave has none yet,
+    // process, raise the bound
+    auto step = [&](Tile<DT, TV, MASK>& T, uint32_t t) __attribute__((always_inline)) {
+        if (gather && t > 0 && mrun == -INFINITY) {
+            mrun = wave_max(tile_max(T, tbase(t)));
+            set_pre();
+        }
+        process(T, tbase(t));
+    };
+    // The steady-state loop refills both buffers unconditionally, so the
+    // compiler's wait for one buffer leaves the other's loads in flight; the
+    // last one to three tiles follow it.
+    auto stream = [&](auto fast_c) __attribute__((always_inline)) {
+        constexpr bool FAST = decltype(fast_c)::value;
+        auto load = [&](Tile<DT, TV, MASK>& T, uint32_t t) __attribute__((always_inline)) {
+            if (FAST) tile_load_fast<DT, TV, MASK, NT>(a, r, rp, tbase(t), hi, T);
+            else tile_load<DT, TV, MASK, NT>(a, r, rp, tbase(t), hi, T);
+        };
+        uint32_t t = 0;
+        for (; t + 3 < ntile; t += 2) {
+            step(b0, t);
+            load(b0, t + 2);
+            if (gather) raise();
+            step(b1, t + 1);
+            load(b1, t + 3);
+            if (gather) raise();
+        }
+        step(b0, t);
+        if (t + 2 < ntile) load(b0, t + 2);
+        if (gather) raise();
+        if (t + 1 < ntile) {
+            step(b1, t + 1);
+            if (gather) raise();
+        }
+        if (t + 2 < ntile) {
+            step(b0, t + 2);
+            if (gather) raise();
+        }
+    };
+    if (fast) stream(std::true_type{});
+    else stream(std::false_type{});
+    // the first element of the best vector that attains the maximum
+    if (tj != NONE) {
+        float v[EPV];
+        vec_vals(traw, tmw, tj, v);
+        uint32_t q0 = NONE;
+#pragma unroll
+        for (int q = EPV - 1; q >= 0; --q)
+            if (v[q] == tm) q0 = (uint32_t)q;
+        ta = tj + q0;
+    }
+    // the special ids' processed values
+    if (special) {
+        auto visit = [&](uint32_t e, float l) {
+            am_merge(tm, ta, l, isnan(l) ? NONE : e);
+            if (gather && l > -INFINITY &&
+                (mrun == -INFINITY || __fmul_rn(__fsub_rn(l, mrun), inv) >= thr))
+                add_cand(e, l);
+            if (gsum_on) gsum_add(l);
+        };
+#pragma unroll
+        for (int k = 0; k < SPK; ++k) {
+            const uint32_t rk = (uint32_t)tid + (uint32_t)k * NT;
+            if (rk < nspec) {
+                const uint32_t e = L.sid[rk];
+                const float l = __uint_as_float(DT == AXS_DTYPE_BF16 ? sraw[k] << 16 : sraw[k]);
+                visit(e, special_value(c, L, e, l, L.cnt[rk], smw[k]));
+            }
+        }
+        if (!ranked || nspec > (uint32_t)SPK * NT)
+            visit_specials<DT, NT, SEGMAX>(a, c, L, ranked, (uint32_t)SPK * NT, r, rp, lo, hi, visit);
+    }
+
+    // segment results
+    __syncthreads();
+    float bm = tm;
+    uint32_t bi = ta;
+    block_argmax<NT>(bm, bi, SL.redf, SL.redu);
+    ChunkStat st;
+    st.m = bi == NONE ? -INFINITY : bm;
+    st.amax = bi;
+    st.flags = sflags;
+    st.gsum = 0.0f;
+    if (gsum_on && isfinite(st.m)) {
+        const float part = isfinite(gm) ? gs * __expf(gm - st.m) : 0.0f;
+        st.gsum = block_sum_f<NT>(part, SL.redf);
+    }
+    const uint32_t n = gather ? SL.ncand : 0u;
+    if (gather && n > CAPC) st.flags |= CS_OVERFLOW;
+
+    if (nseg == 1) {
+        // the whole row is here: decide it in place
+        finish_decide<NT>(a, r, c.p, st.m, st.amax, st.flags, (double)st.gsum, n, SL.u.F, [&](auto&& f) {
+            for (uint32_t i = tid; i < n; i += NT) f(SL.cand[i].id, SL.cand[i].l);
+        });
+        return;
+    }
+
+    if (gather && n <= CAPC) {
+        // publish the candidates within the min-p window of the segment
+        // maximum (<= the row maximum, so still every possible survivor)
+        Cand mine[CPT];
+        uint32_t keep = 0, cnt = 0;
+#pragma unroll
+        for (int k = 0; k < CPT; ++k) {
+            const uint32_t i = (uint32_t)tid + (uint32_t)k * NT;
+            mine[k].id = 0;
+            mine[k].l = 0.0f;
+            if (i < n) {
+                const Cand cd = SL.cand[i];
+                if (__fmul_rn(__fsub_rn(cd.l, st.m), inv) >= thr) {
+                    mine[k] = cd;
+                    keep |= 1u << k;
+                    ++cnt;
+                }
+            }
+        }
+        uint32_t tot;
+        uint32_t pre = block_excl_scan_u32<NT>(cnt, SL.redu, &tot);
+        if (tot > CAPS) {
+            st.flags |= CS_OVERFLOW;
+        } else {
+            Cand* dst = a.pool + ((size_t)r * nseg + si) * CAPS;
+#pragma unroll
+            for (int k = 0; k < CPT; ++k)
+                if ((keep >> k) & 1u) pub_cand(&dst[pre++], mine[k]);
+            st.flags |= tot << 8;
+        }
+    }
+    if (tid == 0) pub_stat(&a.cstat[(size_t)r * nseg + si], st);
+
+    // the last workgroup of the row to get here finishes it; the counter
+    // wraps back to 0 for the next call
+    wait_mem();
+    __syncthreads();
+    if (tid == 0) {
+        const uint32_t old = atomicInc(&a.row_done[r], (uint32_t)nseg - 1u);
+        SL.last = old == (uint32_t)nseg - 1u ? 1u : 0u;
+    }
+    __syncthreads();
+    if (!SL.last) return;
+    finish_row<NT>(a, r, nseg, SL.u.F);
 }
 
 // --------------------------------------------------------------------------
@@ -1004,7 +1489,7 @@ __global__ __launch_bounds__(NT_FIN) void k_finish(KArgs a) {
 // --------------------------------------------------------------------------
 template <int DT, int NV>
 __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
-    __shared__ ProcLds L;
+    __shared__ ProcLds<NT_CHUNK, EX_SEGMAX> L;
     __shared__ uint32_t s_u[NT_CHUNK / 64];
     __shared__ float s_f[NT_CHUNK / 64];
     __shared__ uint32_t s_base;
@@ -1020,7 +1505,13 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
         RowCtx c = make_ctx(a, r);
         Seg<DT, NV> S;
         seg_load<DT, NV>(a, r, lo, hi, a.vec != 0, c.mask_on, S);
-        if (c.any_proc) proc_setup(a, c, lo, hi, L);
+        const bool special = c.cnt_on || c.bias_on || c.ban_on;
+        const char* rp = row_ptr(a, r);
+        bool ranked = true;
+        HistPre<NT_CHUNK> hp;
+        hist_prefetch<NT_CHUNK>(a, c, hp);
+        if (c.any_proc) proc_build<NT_CHUNK, EX_SEGMAX>(a, c, lo, hi, L, hp);
+        if (special) ranked = proc_rank<NT_CHUNK, EX_SEGMAX>(a, c, lo, hi, L, hp);
         const bool minp = rs.mode == M_MINP;
         const float minp_v = c.p.min_p;
         float mg = INFINITY;
@@ -1028,7 +1519,7 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
         float* dense = a.dense + (size_t)r * a.vocab;
         // pass 1: exact probabilities; dense rows are written here, sorted rows
         // only counted
-        seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
+        auto pass1 = [&](uint32_t e, float l) {
             float pr = prob_of(l, rs.m, rs.inv);
             bool keep = true;
             if (minp) {
@@ -1041,7 +1532,9 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
             } else if (v >= rs.pmin) {
                 ++cnt;
             }
-        });
+        };
+        regs_visit<DT, NV>(c, L, lo, S, special, pass1);
+        if (special) visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass1);
         if (rs.sorted) {
             uint32_t tot;
             uint32_t pre = block_excl_scan_u32<NT_CHUNK>(cnt, s_u, &tot);
@@ -1050,11 +1543,13 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
             uint64_t* dst = a.ckey + (size_t)r * a.vocab + s_base + pre;
             uint32_t o = 0;
             // pass 2: write the compacted (p desc, id asc) keys
-            seg_visit<DT, NV>(a, c, L, r, lo, hi, S, [&](uint32_t e, float l) {
+            auto pass2 = [&](uint32_t e, float l) {
                 float pr = prob_of(l, rs.m, rs.inv);
                 if (minp && !(pr >= minp_v)) pr = 0.0f;
                 if (pr >= rs.pmin) dst[o++] = key_pdesc(pr, e);
-            });
+            };
+            regs_visit<DT, NV>(c, L, lo, S, special, pass2);
+            if (special) visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass2);
         }
         if (minp) {
             mg = block_max<NT_CHUNK>(-mg, s_f);
@@ -1117,7 +1612,7 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t key) {
     return b < NBUCKET ? b : NBUCKET - 1;
 }
 
-__global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
+__device__ void exact_row(const KArgs& a) {
     __shared__ uint32_t s_cnt[NBUCKET];
     __shared__ Xd s_w[NT_EX / 64];
     __shared__ uint32_t s_u[NT_EX / 64];
@@ -1125,7 +1620,6 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
     __shared__ uint32_t s_k, s_cross, s_nbig, s_err;
     __shared__ uint32_t s_big[256];
     const int tid = threadIdx.x;
-    if (blockIdx.x >= *a.exact_count) return;
     const int r = (int)a.exact_rows[blockIdx.x];
     const RowState rs = a.rstate[r];
     const axs_sampling_params p = row_params(a, r);
@@ -1278,6 +1772,51 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
         __syncthreads();
     }
 
+    // index-order rows: the kept-set size and the ordered kept lists, by the
+    // whole block
+    uint32_t dkept = 0, dlist = 0;
+    if (!sorted) {
+        const bool mp = rs.mode == M_MINP;
+        uint32_t cnt = 0;
+        for (uint32_t i = tid; i < V; i += NT_EX) cnt += (!mp || dense[i] > 0.0f) ? 1u : 0u;
+        dkept = block_sum_u32<NT_EX>(cnt, s_u);
+        // out_kept: ids with (!min-p || p > 0); ws lists: ids with p > 0
+        const uint32_t cap_o = (a.out_kept && a.out_kept_cap > 0) ? (uint32_t)a.out_kept_cap : 0u;
+        const uint32_t cap_w = a.ws_kept_id ? KEPT_CAP : 0u;
+        uint32_t base_o = 0, base_w = 0;
+        for (uint32_t c0 = 0; c0 < V && (base_o < cap_o || base_w < cap_w); c0 += NT_EX * 8u) {
+            uint32_t fo = 0, fw = 0;
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) {
+                const uint32_t i = c0 + (uint32_t)tid * 8u + q;
+                const float pv = i < V ? dense[i] : 0.0f;
+                if (i < V && (!mp || pv > 0.0f)) fo |= 1u << q;
+                if (pv > 0.0f) fw |= 1u << q;
+            }
+            uint32_t to, tw;
+            uint32_t po = base_o + block_excl_scan_u32<NT_EX>((uint32_t)__popc(fo), s_u, &to);
+            uint32_t pw = base_w + block_excl_scan_u32<NT_EX>((uint32_t)__popc(fw), s_u, &tw);
+#pragma unroll
+            for (uint32_t q = 0; q < 8; ++q) {
+                const uint32_t i = c0 + (uint32_t)tid * 8u + q;
+                if ((fo >> q) & 1u) {
+                    if (po < cap_o) a.out_kept[(size_t)r * cap_o + po] = i;
+                    ++po;
+                }
+                if ((fw >> q) & 1u) {
+                    if (pw < cap_w) {
+                        a.ws_kept_id[(size_t)r * KEPT_CAP + pw] = i;
+                        a.ws_kept_p[(size_t)r * KEPT_CAP + pw] = dense[i];
+                    }
+                    ++pw;
+                }
+            }
+            base_o += to;
+            base_w += tw;
+        }
+        dlist = base_w < cap_w ? base_w : cap_w;
+    }
+
     if (tid != 0) return;
     // decisions (sampling.rs:283-316, 922-952) on the exact running sums
     uint32_t flags = AXS_FLAG_DREW | AXS_FLAG_EXACT_PATH;
@@ -1338,8 +1877,7 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
         if (fmin(up, lo) / (double)F < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
         tok = j;
         pj = dense[j];
-        kept = 0;
-        for (uint32_t i = 0; i < V; ++i) kept += dense[i] > 0.0f || !minp ? 1u : 0u;
+        kept = dkept;
     }
     write_row(a, r, tok, logprob_of(__fdiv_rn(pj, F)), flags);
     if (a.out_kept_count) a.out_kept_count[r] = kept;
@@ -1348,10 +1886,6 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
         if (sorted) {
             uint32_t nw = Lk < cap ? Lk : cap;
             for (uint32_t i = 0; i < nw; ++i) a.out_kept[(size_t)r * cap + i] = pdesc_id(keys[i]);
-        } else {
-            uint32_t o = 0;
-            for (uint32_t i = 0; i < V && o < cap; ++i)
-                if (!minp || dense[i] > 0.0f) a.out_kept[(size_t)r * cap + o++] = i;
         }
     }
     if (a.ws_kept_id) {
@@ -1367,12 +1901,7 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
             // truncate silently
             if (kept > Lk) flags |= AXS_FLAG_ERROR;
         } else {
-            for (uint32_t i = 0; i < V && o < KEPT_CAP; ++i)
-                if (dense[i] > 0.0f) {
-                    a.ws_kept_id[(size_t)r * KEPT_CAP + o] = i;
-                    a.ws_kept_p[(size_t)r * KEPT_CAP + o] = dense[i];
-                    ++o;
-                }
+            o = dlist;
         }
         if (kept > KEPT_CAP) flags |= AXS_FLAG_ERROR;
         a.rstate[r].kept = kept;
@@ -1380,6 +1909,16 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
         a.rstate[r].F = F;
         a.rstate[r].flags = flags;
     }
+}
+
+// One workgroup per listed row.  Every workgroup of the grid also counts
+// itself out; the last one clears the exact-row list for the next call (all
+// of them have read its length by then).
+__global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
+    const uint32_t nex = *a.exact_count;
+    if (blockIdx.x < nex) exact_row(a);
+    __syncthreads();
+    if (threadIdx.x == 0 && atomicInc(a.ex_done, gridDim.x - 1u) == gridDim.x - 1u) *a.exact_count = 0u;
 }
 
 // --------------------------------------------------------------------------
@@ -1600,10 +2139,12 @@ struct axs_context {
     int max_chunks;
     int64_t tmp_stride;
     ChunkStat* cstat;
-    Cand* cand;
+    Cand* pool;             // published candidates [rows, segments, CAPS]
     RowState* rstate;
     uint32_t* exact_rows;
     uint32_t* exact_count;
+    uint32_t* row_done;     // per-row segment counters (atomicInc, wrap to 0)
+    uint32_t* ex_done;      // k_exact_row workgroup counter (atomicInc, wrap to 0)
     float* dense;
     uint64_t* ckey;
     uint64_t* ckey2;
@@ -1646,20 +2187,33 @@ void clear_events(axs_context* c);
 
 void free_ctx(axs_context* c) {
     clear_events(c);
-    void* ptrs[] = {c->cstat, c->cand,  c->rstate, c->exact_rows, c->exact_count, c->dense,  c->ckey,
-                    c->ckey2, c->tmp64, c->sbuf,   c->bend,       c->kept_id,     c->kept_p, c->mtp_tok};
+    void* ptrs[] = {c->cstat, c->pool, c->rstate,  c->exact_rows, c->exact_count,
+                    c->row_done, c->dense, c->ckey, c->ckey2, c->tmp64, c->sbuf, c->bend,
+                    c->kept_id, c->kept_p, c->mtp_tok};
     for (void* q : ptrs)
         if (q) (void)hipFree(q);
     delete c;
 }
 
-// elements per thread-vector and the chunk size for a launch
+// Launch geometry.  k_stream: segments of schunk ids (snch per row) streamed
+// in tiles of 256*tv vectors; the exact path: segments of chunk ids (nch per
+// row), nv vectors per thread, held in registers.
 struct Plan {
     int nv;
     uint32_t chunk;
     int nch;
+    int tv;
+    bool wide;  // one 1024-thread workgroup per row
+    uint32_t schunk;
+    int snch;
     bool vec;
 };
+
+int env_int(const char* name, int dflt) {
+    const char* e = getenv(name);
+    int v = e ? atoi(e) : dflt;
+    return v >= 1 ? v : dflt;
+}
 
 // Segment size: the largest per-thread vector count whose grid still has
 // >= 1024 workgroups (four per CU), so each workgroup keeps up to 64 KB of
@@ -1689,41 +2243,95 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
     }
     pl.chunk = (uint32_t)(NT_CHUNK * pl.nv * epv);
     pl.nch = (int)((vocab + pl.chunk - 1) / pl.chunk);
+    // k_stream: enough (row, segment) workgroups to fill the GPU
+    // (AXS_STREAM_WGS, default 1024: four per CU), segments a multiple of
+    // MIN_CHUNK ids and at most SEG_MAX; AXS_STREAM_TV picks the tile (4 or 8
+    // vectors per thread, default 4)
+    static const int target = env_int("AXS_STREAM_WGS", 1024);
+    static const int tv = env_int("AXS_STREAM_TV", 4) >= 8 ? 8 : 4;
+    // enough rows to give every CU one: each row is one 1024-thread workgroup
+    // that decides it in place (AXS_STREAM_WIDE_ROWS, default 240 rows)
+    static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 240);
+    if (nrows >= wide_rows && (uint32_t)vocab <= ROW_MAX) {
+        pl.wide = true;
+        pl.tv = 4;
+        pl.schunk = (uint32_t)vocab;
+        pl.snch = 1;
+        pl.vec = ((uintptr_t)base % 16 == 0) && ((stride * es) % 16 == 0) &&
+                 (base2 == nullptr || (uintptr_t)base2 % 16 == 0);
+        return pl;
+    }
+    pl.wide = false;
+    int64_t s0 = ((int64_t)target + nrows - 1) / nrows;
+    if (s0 < 1) s0 = 1;
+    int64_t seg = ((int64_t)vocab + s0 - 1) / s0;
+    seg = (seg + MIN_CHUNK - 1) / MIN_CHUNK * MIN_CHUNK;
+    if (seg > (int64_t)SEG_MAX) seg = SEG_MAX;
+    pl.schunk = (uint32_t)seg;
+    pl.snch = (int)(((int64_t)vocab + seg - 1) / seg);
+    pl.tv = tv;
     pl.vec = ((uintptr_t)base % 16 == 0) && ((stride * es) % 16 == 0) &&
              (base2 == nullptr || (uintptr_t)base2 % 16 == 0);
     return pl;
 }
 
 template <int DT, int NV>
-void launch_pair_nv(const KArgs& a, hipStream_t s, bool exact_pass) {
+void launch_exact_nv(const KArgs& a, hipStream_t s) {
     const int64_t total = (int64_t)a.nrows * a.nch;
-    if (!exact_pass) {
-        dim3 grid((unsigned)(((total + 7) / 8) * 8));
-        hipLaunchKernelGGL((k_chunk<DT, NV>), grid, dim3(NT_CHUNK), 0, s, a);
+    int64_t g = total < 1024 ? total : 1024;
+    dim3 grid((unsigned)(g > 0 ? g : 1));
+    hipLaunchKernelGGL((k_exact_mat<DT, NV>), grid, dim3(NT_CHUNK), 0, s, a);
+}
+
+void launch_exact_mat(const Plan& pl, const KArgs& a, hipStream_t s) {
+    if (a.dtype == AXS_DTYPE_BF16) {
+        switch (pl.nv) {
+            case 16: launch_exact_nv<AXS_DTYPE_BF16, 16>(a, s); break;
+            case 8: launch_exact_nv<AXS_DTYPE_BF16, 8>(a, s); break;
+            case 4: launch_exact_nv<AXS_DTYPE_BF16, 4>(a, s); break;
+            case 2: launch_exact_nv<AXS_DTYPE_BF16, 2>(a, s); break;
+            default: launch_exact_nv<AXS_DTYPE_BF16, 1>(a, s); break;
+        }
     } else {
-        int64_t g = total < 1024 ? total : 1024;
-        dim3 grid((unsigned)(g > 0 ? g : 1));
-        hipLaunchKernelGGL((k_exact_mat<DT, NV>), grid, dim3(NT_CHUNK), 0, s, a);
+        switch (pl.nv) {
+            case 16: launch_exact_nv<AXS_DTYPE_F32, 16>(a, s); break;
+            case 8: launch_exact_nv<AXS_DTYPE_F32, 8>(a, s); break;
+            case 4: launch_exact_nv<AXS_DTYPE_F32, 4>(a, s); break;
+            default: launch_exact_nv<AXS_DTYPE_F32, 2>(a, s); break;
+        }
     }
 }
 
-void launch_chunkish(const Plan& pl, const KArgs& a, hipStream_t s, bool exact_pass) {
-    if (a.dtype == AXS_DTYPE_BF16) {
-        switch (pl.nv) {
-            case 16: launch_pair_nv<AXS_DTYPE_BF16, 16>(a, s, exact_pass); break;
-            case 8: launch_pair_nv<AXS_DTYPE_BF16, 8>(a, s, exact_pass); break;
-            case 4: launch_pair_nv<AXS_DTYPE_BF16, 4>(a, s, exact_pass); break;
-            case 2: launch_pair_nv<AXS_DTYPE_BF16, 2>(a, s, exact_pass); break;
-            default: launch_pair_nv<AXS_DTYPE_BF16, 1>(a, s, exact_pass); break;
-        }
-    } else {
-        switch (pl.nv) {
-            case 16: launch_pair_nv<AXS_DTYPE_F32, 16>(a, s, exact_pass); break;
-            case 8: launch_pair_nv<AXS_DTYPE_F32, 8>(a, s, exact_pass); break;
-            case 4: launch_pair_nv<AXS_DTYPE_F32, 4>(a, s, exact_pass); break;
-            default: launch_pair_nv<AXS_DTYPE_F32, 2>(a, s, exact_pass); break;
-        }
-    }
+template <int DT, int TV, int NT, uint32_t SEGMAX>
+void launch_stream_tv(const KArgs& a, hipStream_t s) {
+    const int64_t total = (int64_t)a.nrows * a.snch;
+    dim3 grid((unsigned)(((total + 7) / 8) * 8));
+    if (a.mask) hipLaunchKernelGGL((k_stream<DT, TV, true, NT, SEGMAX>), grid, dim3(NT), 0, s, a);
+    else hipLaunchKernelGGL((k_stream<DT, TV, false, NT, SEGMAX>), grid, dim3(NT), 0, s, a);
+}
+
+template <int DT>
+void launch_stream_dt(const Plan& pl, const KArgs& a, hipStream_t s) {
+    if (pl.wide) launch_stream_tv<DT, 4, 1024, ROW_MAX>(a, s);
+    else if (pl.tv == 8) launch_stream_tv<DT, 8, NT_CHUNK, SEG_MAX>(a, s);
+    else launch_stream_tv<DT, 4, NT_CHUNK, SEG_MAX>(a, s);
+}
+
+void launch_stream(const Plan& pl, const KArgs& a, hipStream_t s) {
+    if (a.dtype == AXS_DTYPE_BF16) launch_stream_dt<AXS_DTYPE_BF16>(pl, a, s);
+    else launch_stream_dt<AXS_DTYPE_F32>(pl, a, s);
+}
+
+// geometry fields of KArgs from the plan
+int apply_plan(KArgs& a, const Plan& pl) {
+    if (pl.nch > (int)MAX_SEGS || pl.snch > (int)MAX_SEGS)
+        return fail(AXS_E_UNSUPPORTED, "vocab too large (more than 1024 segments)");
+    a.nch = pl.nch;
+    a.chunk = (int32_t)pl.chunk;
+    a.snch = pl.snch;
+    a.schunk = (int32_t)pl.schunk;
+    a.vec = pl.vec ? 1 : 0;
+    return AXS_OK;
 }
 
 void clear_events(axs_context* c) {
@@ -1754,10 +2362,12 @@ void timed(axs_context* c, int kind, hipStream_t s, F&& launch) {
 
 void fill_ws(KArgs& a, axs_context* c) {
     a.cstat = c->cstat;
-    a.cand = c->cand;
+    a.pool = c->pool;
     a.rstate = c->rstate;
     a.exact_rows = c->exact_rows;
     a.exact_count = c->exact_count;
+    a.row_done = c->row_done;
+    a.ex_done = c->ex_done;
     a.dense = c->dense;
     a.ckey = c->ckey;
     a.ckey2 = c->ckey2;
@@ -1767,18 +2377,13 @@ void fill_ws(KArgs& a, axs_context* c) {
     a.tmp_stride = c->tmp_stride;
 }
 
-// the four-kernel pipeline over a.nrows rows
+// the three-kernel pipeline over a.nrows rows
 int run_pipeline(axs_context* c, KArgs& a, const Plan& pl, hipStream_t s) {
-    if (pl.nch > (int)MAX_SEGS) return fail(AXS_E_UNSUPPORTED, "vocab too large (more than 1024 segments)");
-    a.nch = pl.nch;
-    a.chunk = (int32_t)pl.chunk;
-    a.vec = pl.vec ? 1 : 0;
+    int rc = apply_plan(a, pl);
+    if (rc) return rc;
     fill_ws(a, c);
-    timed(c, AXS_KERNEL_CHUNK, s, [&] { launch_chunkish(pl, a, s, false); });
-    timed(c, AXS_KERNEL_FINISH, s, [&] {
-        hipLaunchKernelGGL(k_finish, dim3((unsigned)a.nrows), dim3(NT_FIN), 0, s, a);
-    });
-    timed(c, AXS_KERNEL_EXACT_MAT, s, [&] { launch_chunkish(pl, a, s, true); });
+    timed(c, AXS_KERNEL_STREAM, s, [&] { launch_stream(pl, a, s); });
+    timed(c, AXS_KERNEL_EXACT_MAT, s, [&] { launch_exact_mat(pl, a, s); });
     timed(c, AXS_KERNEL_EXACT_ROW, s, [&] {
         hipLaunchKernelGGL(k_exact_row, dim3((unsigned)a.nrows), dim3(NT_EX), 0, s, a);
     });
@@ -1818,8 +2423,9 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
     size_t R = (size_t)max_batch, Vv = (size_t)max_vocab;
     int rc = AXS_OK;
     if ((rc = dalloc(&c->cstat, R * c->max_chunks)) ||
-        (rc = dalloc(&c->cand, R * c->max_chunks * CAPC)) || (rc = dalloc(&c->rstate, R)) ||
+        (rc = dalloc(&c->pool, R * c->max_chunks * CAPS)) || (rc = dalloc(&c->rstate, R)) ||
         (rc = dalloc(&c->exact_rows, R)) || (rc = dalloc(&c->exact_count, 1)) ||
+        (rc = dalloc(&c->row_done, R + 1)) ||
         (rc = dalloc(&c->dense, R * Vv)) || (rc = dalloc(&c->ckey, R * Vv)) ||
         (rc = dalloc(&c->ckey2, R * Vv)) || (rc = dalloc(&c->tmp64, R * (size_t)c->tmp_stride)) ||
         (rc = dalloc(&c->sbuf, R * Vv)) || (rc = dalloc(&c->bend, R * NBUCKET)) ||
@@ -1827,6 +2433,14 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
         (rc = dalloc(&c->mtp_tok, R))) {
         free_ctx(c);
         return rc;
+    }
+    c->ex_done = c->row_done + R;
+    // the counters start at zero; every call leaves them at zero again
+    if (hipMemset(c->row_done, 0, (R + 1) * sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(c->exact_count, 0, sizeof(uint32_t)) != hipSuccess ||
+        hipDeviceSynchronize() != hipSuccess) {
+        free_ctx(c);
+        return fail(AXS_E_HIP, "clearing the workspace counters failed");
     }
     *out = c;
     return AXS_OK;
@@ -1911,16 +2525,11 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
     a.out_ids = out_ids;
     a.out_lp = out_logprob;
     Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
-    if (pl.nch > (int)MAX_SEGS) return fail(AXS_E_UNSUPPORTED, "vocab too large (more than 1024 segments)");
-    a.nch = pl.nch;
-    a.chunk = (int32_t)pl.chunk;
-    a.vec = pl.vec ? 1 : 0;
+    int rc = apply_plan(a, pl);
+    if (rc) return rc;
     fill_ws(a, ctx);
     hipStream_t s = (hipStream_t)stream;
-    timed(ctx, AXS_KERNEL_CHUNK, s, [&] { launch_chunkish(pl, a, s, false); });
-    timed(ctx, AXS_KERNEL_FINISH, s, [&] {
-        hipLaunchKernelGGL(k_finish, dim3((unsigned)batch), dim3(NT_FIN), 0, s, a);
-    });
+    timed(ctx, AXS_KERNEL_STREAM, s, [&] { launch_stream(pl, a, s); });
     AXS_HIP_CHECK(hipGetLastError());
     return AXS_OK;
 }

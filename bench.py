@@ -8,8 +8,9 @@ the 256 MB MALL) rotate so repeated steps do not read from the Infinity Cache.
 
 Prints one JSON line:
   value      rows/s of the whole step (all kernels), timed over K steps
-  roofline   the single HBM pass (k_chunk): algorithmic bytes per launch /
-             its average duration from hipEvents on its launch stream
+  roofline   the single HBM pass (k_stream, which also decides the rows):
+             algorithmic bytes per launch / its average duration from
+             hipEvents on its launch stream
   cpu_baseline  the CPU restatement of the reference sampler (oracle/, the
              reference's own Rust cannot be built here) on a bounded sample
              of the same rows, timed on this host
@@ -119,7 +120,7 @@ def main():
         if n:
             kern[name] = {"avg_us": 1e3 * ms / n, "launches": n}
     s.timing(False)
-    chunk_us = kern["k_chunk"]["avg_us"]
+    chunk_us = kern["k_stream"]["avg_us"]
     alg = w.algorithmic_bytes()
     achieved = alg / (chunk_us * 1e-6) / 1e9
     step_gbs = alg / (ms_step * 1e-3) / 1e9
@@ -161,7 +162,7 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "k_chunk",
+            "kernel": "k_stream",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

@@ -230,12 +230,12 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
 /* Per-kernel timing, for benchmarks (no counterpart in the reference).  While
  * enabled, every kernel the context launches is bracketed by hipEvents
  * recorded on its launch stream.  Enabling clears earlier records. */
-#define AXS_KERNEL_CHUNK     0  /* the single pass over the logits    */
-#define AXS_KERNEL_FINISH    1  /* per-row merge and decisions        */
-#define AXS_KERNEL_EXACT_MAT 2  /* exact path: second pass            */
-#define AXS_KERNEL_EXACT_ROW 3  /* exact path: sort + exact sums      */
-#define AXS_KERNEL_MTP       4  /* MTP accept / residual / bonus      */
-#define AXS_KERNEL_COUNT     5
+#define AXS_KERNEL_STREAM    0  /* the single pass over the logits, with
+                                   the per-row decisions                */
+#define AXS_KERNEL_EXACT_MAT 1  /* exact path: second pass            */
+#define AXS_KERNEL_EXACT_ROW 2  /* exact path: sort + exact sums      */
+#define AXS_KERNEL_MTP       3  /* MTP accept / residual / bonus      */
+#define AXS_KERNEL_COUNT     4
 int axs_timing_enable(axs_context* ctx, int enable);
 /* Waits for the recorded events of one kernel class and returns their summed
  * duration in milliseconds and the number of launches since enabling. */
