@@ -125,6 +125,25 @@ __device__ __forceinline__ float wave_max(float v) {
     return v;
 }
 
+// Maximum over the 64 lanes with DPP row operations instead of LDS
+// permutes: pairs, quads, half rows, rows, then rows 1 and 3 take the rows
+// below them and row 3 the first half; lane 63 holds the result, returned
+// wave-uniform.  Every lane must be active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float dpp_f(float x) {
+    const int v = __float_as_int(x);
+    return __int_as_float(__builtin_amdgcn_update_dpp(v, v, CTRL, ROWS, 0xF, false));
+}
+__device__ __forceinline__ float wave_max_dpp(float x) {
+    x = fmaxf(x, dpp_f<0xB1, 0xF>(x));   // quad_perm [1,0,3,2]
+    x = fmaxf(x, dpp_f<0x4E, 0xF>(x));   // quad_perm [2,3,0,1]
+    x = fmaxf(x, dpp_f<0x141, 0xF>(x));  // row_half_mirror
+    x = fmaxf(x, dpp_f<0x140, 0xF>(x));  // row_mirror
+    x = fmaxf(x, dpp_f<0x142, 0xA>(x));  // row_bcast:15 into rows 1, 3
+    x = fmaxf(x, dpp_f<0x143, 0xC>(x));  // row_bcast:31 into rows 2, 3
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, d, 64));

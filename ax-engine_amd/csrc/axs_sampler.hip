@@ -53,7 +53,7 @@ constexpr uint32_t ROW_MAX = 262144;  // ids per row, one 1024-thread workgroup 
 constexpr uint32_t EX_SEGMAX = 32768; // ids per exact-path segment
 constexpr uint32_t MAX_SEGS = 1024;   // segments per row (upper bound)
 constexpr int NT_FIN = 256;
-constexpr uint32_t FIN_CAP = 2048;    // min-p candidates merged per row
+constexpr uint32_t FIN_CAP = 2048;    // min-p candidates merged per row (1024-thread rows)
 constexpr uint32_t CAPS = 256;        // published candidates per segment (power of 2)
 constexpr int NT_EX = 1024;
 constexpr uint32_t NBUCKET = 13312;   // 13 per thread; covers p in [2^-24, 1]
@@ -266,7 +266,7 @@ template <int NT, uint32_t SEGMAX>
 struct ProcLds {
     static constexpr uint32_t NW = SEGMAX / 32;      // bitmap words
     static constexpr uint32_t PW = NW / NT;          // bitmap words per thread
-    static constexpr uint32_t RCAP = SEGMAX / 32;    // ranked special ids
+    static constexpr uint32_t RCAP = NT >= 1024 ? SEGMAX / 32 : SEGMAX / 64;  // ranked special ids
     static constexpr uint32_t BCAP = NT >= 1024 ? 1024u : BIAS_LDS;  // bias entries
     uint32_t spec[NW];
     uint16_t pre[NW];
@@ -468,24 +468,34 @@ __device__ __forceinline__ bool proc_rank(const KArgs& a, const RowCtx& c, uint3
     using PL = ProcLds<NT, SEGMAX>;
     const int tid = threadIdx.x;
     const uint32_t nw = (hi - lo + 31u) / 32u;
-    uint32_t pc[PL::PW];
+    static_assert(PL::PW % 4 == 0, "bitmap words per thread");
+    // thread t owns words [t*PW, t*PW + PW), read four at a time as 16-byte
+    // vectors (no bank conflicts); counted first, ranked after the scan
+    const uint32_t w0 = (uint32_t)tid * PL::PW;
     uint32_t cnt = 0;
 #pragma unroll
-    for (uint32_t k = 0; k < PL::PW; ++k) {
-        const uint32_t wi = (uint32_t)tid * PL::PW + k;
-        pc[k] = wi < nw ? (uint32_t)__popc(L.spec[wi]) : 0u;
-        cnt += pc[k];
+    for (uint32_t k = 0; k < PL::PW; k += 4) {
+        const u32x4 x = *(const u32x4*)&L.spec[w0 + k];
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) cnt += w0 + k + q < nw ? (uint32_t)__popc(x[q]) : 0u;
     }
     uint32_t n;
     uint32_t pre = block_excl_scan_u32<NT>(cnt, L.scan, &n);
     const bool ranked = n <= PL::RCAP;
+    uint32_t* pre32 = (uint32_t*)L.pre + w0 / 2;
 #pragma unroll
-    for (uint32_t k = 0; k < PL::PW; ++k) {
-        const uint32_t wi = (uint32_t)tid * PL::PW + k;
-        if (wi < nw) {
-            L.pre[wi] = (uint16_t)(pre < 65535u ? pre : 65535u);
+    for (uint32_t k = 0; k < PL::PW; k += 4) {
+        const u32x4 x = *(const u32x4*)&L.spec[w0 + k];
+        uint32_t pk[2];
+#pragma unroll
+        for (uint32_t q = 0; q < 4; ++q) {
+            const uint32_t wi = w0 + k + q;
+            const uint32_t bits0 = wi < nw ? x[q] : 0u;
+            const uint32_t p16 = pre < 65535u ? pre : 65535u;
+            if (q & 1u) pk[q / 2] |= p16 << 16;
+            else pk[q / 2] = p16;
             if (ranked) {
-                uint32_t bits = L.spec[wi];
+                uint32_t bits = bits0;
                 uint32_t rk = pre;
                 while (bits) {
                     const uint32_t b = (uint32_t)__ffs((int)bits) - 1u;
@@ -495,8 +505,9 @@ __device__ __forceinline__ bool proc_rank(const KArgs& a, const RowCtx& c, uint3
                     ++rk;
                 }
             }
+            pre += (uint32_t)__popc(bits0);
         }
-        pre += pc[k];
+        *(uint2*)&pre32[k / 2] = make_uint2(pk[0], pk[1]);
     }
     if (tid == 0) L.nspec = n;
     __syncthreads();
@@ -754,9 +765,22 @@ __device__ __forceinline__ float lane_f(float v, int k) {
 // --------------------------------------------------------------------------
 // Row finish
 // --------------------------------------------------------------------------
+// first index i in [lo, hi) with S[i] >= t for non-decreasing S (hi if none)
+__device__ __forceinline__ uint32_t first_ge(const float* S, uint32_t lo, uint32_t hi, float t) {
+    uint32_t a = lo, b = hi;
+    while (a < b) {
+        uint32_t mid = a + (b - a) / 2;
+        if (S[mid] >= t) b = mid;
+        else a = mid + 1;
+    }
+    return a;
+}
+
 template <int NT>
 struct FinLds {
-    uint64_t key[FIN_CAP];
+    static constexpr uint32_t CAP = NT >= 1024 ? FIN_CAP : FIN_CAP / 2;
+    uint64_t key[CAP];
+    float S[CAP];            // running sums over the sorted candidates
     uint32_t cnt[MAX_SEGS];  // candidates published by each segment
     float rf[NT / 64];
     uint32_t ru[NT / 64];
@@ -764,99 +788,76 @@ struct FinLds {
     uint32_t n;
 };
 
-// Sequential decisions over n sorted candidates (F.key), the reference's own
-// f32 loops (sampling.rs:283-316, 922-952), run by wave 0: the candidates are
-// read 64 at a time, one per lane, and the running f32 sums walk them with
-// readlane so no step of the chain waits on LDS.
+// Decisions over n sorted candidates (F.key), run by wave 0.  The reference
+// walks the candidates with f32 running sums (sampling.rs:283-316, 922-952):
+// the top-p total, the nucleus cut, the filtered sum and the draw all read
+// the same running sums S[i] = fl(S[i-1] + p_i) in the same order, so one
+// sequential pass computes them (lane 0) and the cuts are binary searches.
 template <int NT>
 __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_sampling_params& p, uint32_t mode,
-                                              bool sorted, const FinLds<NT>& F, uint32_t n, uint32_t flags0) {
+                                              bool sorted, FinLds<NT>& F, uint32_t n, uint32_t flags0) {
     const int lane = threadIdx.x & 63;
     auto P = [&](uint64_t k) { return sorted ? pdesc_p(k) : idasc_p(k); };
     auto ID = [&](uint64_t k) { return sorted ? pdesc_id(k) : idasc_id(k); };
-    uint32_t flags = flags0 | AXS_FLAG_DREW;
     const uint32_t L = n;
-    uint32_t nk = L;
-    if (sorted && topp_active(p)) {
-        // top-p over the full candidate mass (sampling.rs:931-945)
-        float total = 0.0f;
-        for (uint32_t b = 0; b < L; b += 64) {
-            const uint32_t i = b + lane;
-            const float pv = i < L ? P(F.key[i]) : 0.0f;
-            const uint32_t cnt = min(64u, L - b);
-            for (uint32_t k = 0; k < cnt; ++k) total = __fadd_rn(total, lane_f(pv, (int)k));
-        }
-        const float cutoff = __fmul_rn(p.top_p, total);
-        float cum = 0.0f, prev = 0.0f;
-        uint32_t keep = 0;
-        bool done = false;
-        for (uint32_t b = 0; b < L && !done; b += 64) {
-            const uint32_t i = b + lane;
-            const float pv = i < L ? P(F.key[i]) : 0.0f;
-            const uint32_t cnt = min(64u, L - b);
-            for (uint32_t k = 0; k < cnt; ++k) {
-                prev = cum;
-                cum = __fadd_rn(cum, lane_f(pv, (int)k));
-                keep += 1;
-                if (cum >= cutoff) {
-                    done = true;
-                    break;
-                }
-            }
-        }
-        nk = keep > 1 ? keep : 1;
-        const double up = (double)cum - (double)cutoff;
-        const double lo = keep > 1 ? (double)cutoff - (double)prev : INFINITY;
-        if (fmin(up, lo) / (double)total < 1e-6 && (p.top_k == 0 || nk <= p.top_k))
-            flags |= AXS_FLAG_NEAR_NUCLEUS;
-    }
-    uint32_t kept = nk;
-    if (sorted && p.top_k > 0 && kept > p.top_k) kept = p.top_k;
-    if (sorted && kept < L) {
-        const float pa = P(F.key[kept - 1]);
-        const float pb = P(F.key[kept]);
-        // near but not identical probabilities across the cut (identical ones
-        // come from equal logits and are ordered by id everywhere)
-        if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
-    }
-    float Fs = 0.0f;
-    for (uint32_t b = 0; b < kept; b += 64) {
-        const uint32_t i = b + lane;
-        const float pv = i < kept ? P(F.key[i]) : 0.0f;
-        const uint32_t cnt = min(64u, kept - b);
-        for (uint32_t k = 0; k < cnt; ++k) Fs = __fadd_rn(Fs, lane_f(pv, (int)k));
-    }
-    const float u = row_uniform(a, r, p);
-    const float thr = __fmul_rn(u, Fs);
-    float cum = 0.0f, prev = 0.0f;
-    uint32_t j = kept;
-    for (uint32_t b = 0; b < kept && j == kept; b += 64) {
-        const uint32_t i = b + lane;
-        const float pv = i < kept ? P(F.key[i]) : 0.0f;
-        const uint32_t cnt = min(64u, kept - b);
-        for (uint32_t k = 0; k < cnt; ++k) {
-            prev = cum;
-            cum = __fadd_rn(cum, lane_f(pv, (int)k));
-            if (cum >= thr) {
-                j = b + k;
-                break;
-            }
-        }
-    }
-    if (j == kept) {
-        // last maximum (sampling.rs:310-315); unreachable for u <= 1
-        float bp = -1.0f;
-        for (uint32_t i = 0; i < kept; ++i)
-            if (P(F.key[i]) >= bp) {
-                bp = P(F.key[i]);
-                j = i;
-            }
-    } else {
-        const double up = (double)cum - (double)thr;
-        const double lo = j > 0 ? (double)thr - (double)prev : INFINITY;
-        if (fmin(up, lo) / (double)Fs < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
-    }
+    uint32_t kept = 0;
     if (lane == 0) {
+        float acc = 0.0f;
+        uint32_t i = 0;
+        for (; i + 8 <= L; i += 8) {
+            float pv[8];
+#pragma unroll
+            for (int q = 0; q < 8; ++q) pv[q] = P(F.key[i + q]);
+#pragma unroll
+            for (int q = 0; q < 8; ++q) {
+                acc = __fadd_rn(acc, pv[q]);
+                F.S[i + q] = acc;
+            }
+        }
+        for (; i < L; ++i) {
+            acc = __fadd_rn(acc, P(F.key[i]));
+            F.S[i] = acc;
+        }
+        const float* S = F.S;
+        uint32_t flags = flags0 | AXS_FLAG_DREW;
+        uint32_t nk = L;
+        if (sorted && topp_active(p)) {
+            // top-p over the full candidate mass (sampling.rs:931-945)
+            const float total = S[L - 1];
+            const float cutoff = __fmul_rn(p.top_p, total);
+            const uint32_t j = first_ge(S, 0, L, cutoff);
+            nk = j < L ? j + 1 : L;
+            const double up = (double)S[nk - 1] - (double)cutoff;
+            const double lo = nk >= 2 ? (double)cutoff - (double)S[nk - 2] : INFINITY;
+            if (fmin(up, lo) / (double)total < 1e-6 && (p.top_k == 0 || nk <= p.top_k))
+                flags |= AXS_FLAG_NEAR_NUCLEUS;
+        }
+        kept = nk;
+        if (sorted && p.top_k > 0 && kept > p.top_k) kept = p.top_k;
+        if (sorted && kept < L) {
+            const float pa = P(F.key[kept - 1]);
+            const float pb = P(F.key[kept]);
+            // near but not identical probabilities across the cut (identical
+            // ones come from equal logits and are ordered by id everywhere)
+            if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
+        }
+        const float Fs = S[kept - 1];
+        const float u = row_uniform(a, r, p);
+        const float thr = __fmul_rn(u, Fs);
+        uint32_t j = first_ge(S, 0, kept, thr);
+        if (j == kept) {
+            // last maximum (sampling.rs:310-315); unreachable for u <= 1
+            float bp = -1.0f;
+            for (uint32_t i2 = 0; i2 < kept; ++i2)
+                if (P(F.key[i2]) >= bp) {
+                    bp = P(F.key[i2]);
+                    j = i2;
+                }
+        } else {
+            const double up = (double)S[j] - (double)thr;
+            const double lo = j > 0 ? (double)thr - (double)S[j - 1] : INFINITY;
+            if (fmin(up, lo) / (double)Fs < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
+        }
         const float pj = P(F.key[j]);
         write_row(a, r, ID(F.key[j]), logprob_of(__fdiv_rn(pj, Fs)), flags);
         if (a.out_kept_count) a.out_kept_count[r] = kept;
@@ -867,6 +868,7 @@ __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_s
             a.rstate[r].flags = flags;
         }
     }
+    kept = (uint32_t)__builtin_amdgcn_readlane((int)kept, 0);
     if (a.out_kept && a.out_kept_cap > 0) {
         const uint32_t nw = kept < (uint32_t)a.out_kept_cap ? kept : (uint32_t)a.out_kept_cap;
         for (uint32_t i = lane; i < nw; i += 64) a.out_kept[(size_t)r * a.out_kept_cap + i] = ID(F.key[i]);
@@ -929,7 +931,7 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
     }
     const bool minp = mode == M_MINP;
     const bool sorted = minp ? filters_enabled(p) : (mode != M_FAST);
-    bool exact = !minp || (fl & CS_OVERFLOW) || ncand > FIN_CAP;
+    bool exact = !minp || (fl & CS_OVERFLOW) || ncand > FinLds<NT>::CAP;
     if (!exact) {
         // min-p survivors: p = exp((l - m) / T) >= min_p (cutoff = min_p *
         // max_prob, max_prob = 1)
@@ -948,24 +950,28 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
         if (n == 0) exact = true;  // (unreachable: the maximum itself has p = 1)
         if (!exact) {
             const uint32_t flags0 = mg < 1e-6f ? AXS_FLAG_NEAR_MINP : 0u;
-            if (n <= 64) {
-                if (tid < 64) {
-                    uint64_t k = (uint32_t)tid < n ? F.key[tid] : 0ull;
-                    k = wave_sort_desc(k);
-                    F.key[tid] = k;
-                }
-            } else if (n <= 256) {
-                if (tid < 64) {
-                    uint64_t k[4];
+            constexpr uint32_t RS_MAX = 512;  // rank sort up to this many keys
+            if (n <= RS_MAX) {
+                // rank sort: each key's rank is the number of larger keys
+                // (keys are distinct), read from LDS by every thread at once
+                constexpr int KPT = (int)((RS_MAX + NT - 1) / NT);
+                uint64_t mk[KPT];
+                uint32_t rk[KPT];
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const uint32_t i = (uint32_t)(j * 64 + tid);
-                        k[j] = i < n ? F.key[i] : 0ull;
-                    }
-                    wave_sort_desc4(k);
-#pragma unroll
-                    for (int j = 0; j < 4; ++j) F.key[j * 64 + tid] = k[j];
+                for (int k = 0; k < KPT; ++k) {
+                    const uint32_t i = (uint32_t)tid + (uint32_t)k * NT;
+                    mk[k] = i < n ? F.key[i] : 0ull;
+                    rk[k] = 0;
                 }
+                for (uint32_t j = 0; j < n; ++j) {
+                    const uint64_t kj = F.key[j];
+#pragma unroll
+                    for (int k = 0; k < KPT; ++k) rk[k] += kj > mk[k] ? 1u : 0u;
+                }
+                __syncthreads();
+#pragma unroll
+                for (int k = 0; k < KPT; ++k)
+                    if ((uint32_t)tid + (uint32_t)k * NT < n) F.key[rk[k]] = mk[k];
             } else {
                 const uint32_t np2 = next_pow2(n);
                 for (uint32_t i = n + tid; i < np2; i += NT) F.key[i] = 0ull;
@@ -1053,12 +1059,15 @@ struct Tile {
     uint32_t mw[MASK ? TV : 1];
 };
 
+// The loads of one wave's chunk of a tile: `slot` is the thread's position in
+// the tile (chunk's wave slot * 64 + lane); vector j covers ids
+// t0 + (j*NT + slot)*EPV + [0, EPV).  Ids >= hi read as NaN.
 template <int DT, int TV, bool MASK, int NT>
 __device__ __forceinline__ void tile_load(const KArgs& a, int r, const char* rp, uint32_t t0, uint32_t hi,
-                                          Tile<DT, TV, MASK>& T) {
+                                          uint32_t slot, Tile<DT, TV, MASK>& T) {
     constexpr int EPV = Ev<DT>::EPV;
     constexpr uint32_t TILE = (uint32_t)NT * TV * EPV;
-    const int tid = threadIdx.x;
+    const uint32_t tid = slot;
     if (a.vec && t0 + TILE <= hi) {
         // whole tile in range (uniform): 16-byte nontemporal loads only
 #pragma unroll
@@ -1101,15 +1110,17 @@ __device__ __forceinline__ void tile_load(const KArgs& a, int r, const char* rp,
 // every lane loads, the lanes past the end re-read the tile's first vector
 // (their values are discarded by index), so the loads are the same on every
 // path and the compiler can keep the next tile in flight.
+// (valid = false: a chunk past the end of the work; every lane reads the
+// row's first vector, one cache line, so the loads still issue)
 template <int DT, int TV, bool MASK, int NT>
 __device__ __forceinline__ void tile_load_fast(const KArgs& a, int r, const char* rp, uint32_t t0, uint32_t hi,
-                                               Tile<DT, TV, MASK>& T) {
+                                               uint32_t slot, bool valid, Tile<DT, TV, MASK>& T) {
     constexpr int EPV = Ev<DT>::EPV;
-    const int tid = threadIdx.x;
 #pragma unroll
     for (int j = 0; j < TV; ++j) {
-        uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+        uint32_t e0 = t0 + ((uint32_t)j * NT + slot) * EPV;
         e0 = e0 < hi ? e0 : t0;
+        if (!valid) e0 = 0u;
         T.raw[j] = __builtin_nontemporal_load((const u32x4*)(rp + (size_t)e0 * (EPV == 8 ? 2 : 4)));
         if (MASK) T.mw[j] = a.mask[(size_t)r * a.mask_stride + (e0 >> 5)];
     }
@@ -1123,14 +1134,16 @@ struct StreamLds {
         FinLds<NT> F;
     } u;
     Cand cand[CAPC];
+    u32x4 xt[256];  // bit pattern of a vector → per-word mask of its marked elements
     float red[NT / 64];
     float redf[NT / 64];
     uint32_t redu[NT / 64];
     uint32_t ncand;
+    uint32_t next;  // next unclaimed chunk
     uint32_t last;
 };
 
-template <int DT, int TV, bool MASK, int NT, uint32_t SEGMAX>
+template <int DT, int TV, bool MASK, int NT, uint32_t SEGMAX, bool FAST>
 __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
     using SLT = StreamLds<NT, SEGMAX>;
     constexpr int EPV = Ev<DT>::EPV;
@@ -1163,19 +1176,50 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
 
     // loads in flight before anything waits: the segment's first two tiles,
     // then the first round of the repetition window
-    const bool fast = a.vec && (hi % EPV) == 0;
+    // The segment is cut into chunks, one wave's share of a tile (64 lanes x
+    // TV vectors): chunk c is slot c % NW of tile c / NW.  Each wave starts
+    // with chunks wv and NW + wv and then takes the next unclaimed chunk from
+    // an LDS counter, so waves that get their data sooner do more of the work.
+    constexpr uint32_t NW = NT / 64;
+    const uint32_t nchunk = ntile * NW;
+    auto chunk_t0 = [&](uint32_t ch) { return tbase(ch / NW); };
+    auto chunk_slot = [&](uint32_t ch) { return (ch % NW) * 64u + (uint32_t)lane; };
+    auto load = [&](Tile<DT, TV, MASK>& T, uint32_t ch) __attribute__((always_inline)) {
+        const bool valid = ch < nchunk;  // wave-uniform
+        if (FAST) {
+            tile_load_fast<DT, TV, MASK, NT>(a, r, rp, valid ? chunk_t0(ch) : lo, hi, valid ? chunk_slot(ch) : 0u,
+                                             valid, T);
+        } else {
+            const uint32_t t0 = valid ? chunk_t0(ch) : lo;
+            tile_load<DT, TV, MASK, NT>(a, r, rp, t0, valid ? hi : t0, valid ? chunk_slot(ch) : 0u, T);
+        }
+    };
+    // FAST: 16-byte aligned rows whose length is a multiple of EPV
+    uint32_t c0 = (uint32_t)wv, c1 = NW + (uint32_t)wv;
     Tile<DT, TV, MASK> b0, b1;
-    if (fast) {
-        tile_load_fast<DT, TV, MASK, NT>(a, r, rp, tbase(0), hi, b0);
-        if (ntile > 1) tile_load_fast<DT, TV, MASK, NT>(a, r, rp, tbase(1), hi, b1);
-    } else {
-        tile_load<DT, TV, MASK, NT>(a, r, rp, tbase(0), hi, b0);
-        if (ntile > 1) tile_load<DT, TV, MASK, NT>(a, r, rp, tbase(1), hi, b1);
-    }
+    load(b0, c0);
+    load(b1, c1);
+    if (tid == 0) SL.next = 2u * NW;
     const RowCtx c = make_ctx(a, r);
     HistPre<NT> hp;
     hist_prefetch<NT>(a, c, hp);
     const bool special = c.cnt_on || c.bias_on || c.ban_on;
+    if (special || MASK) {
+        // expansion table: bit q of an index marks element q of a vector; the
+        // entry holds, per 32-bit word of the vector, all ones over the
+        // marked elements (the barriers of proc_build publish it)
+        for (uint32_t i = tid; i < 256u; i += NT) {
+            u32x4 m;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (DT == AXS_DTYPE_BF16)
+                    m[k] = (((i >> (2 * k)) & 1u) ? 0x0000FFFFu : 0u) | (((i >> (2 * k + 1)) & 1u) ? 0xFFFF0000u : 0u);
+                else
+                    m[k] = ((i >> k) & 1u) ? 0xFFFFFFFFu : 0u;
+            }
+            SL.xt[i] = m;
+        }
+    }
     if (c.any_proc) proc_build<NT, SEGMAX>(a, c, lo, hi, L, hp);
     bool ranked = true;
     if (special) ranked = proc_rank<NT, SEGMAX>(a, c, lo, hi, L, hp);
@@ -1242,22 +1286,24 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
     };
     // the EPV logits of a vector as the processors see them, with the special
     // ids as NaN: never a maximum, never gathered
-    auto vec_vals = [&](const u32x4& raw, uint32_t mw, uint32_t e0, float* v) {
-#pragma unroll
-        for (int q = 0; q < EPV; ++q) v[q] = unpack<DT>(raw, q);
+    // (on the raw words: disallowed elements become -inf and special ones an
+    // all-ones pattern, which is a NaN in both formats)
+    constexpr uint32_t EMASK = (1u << EPV) - 1u;
+    constexpr uint32_t NINF = DT == AXS_DTYPE_BF16 ? 0xFF80FF80u : 0xFF800000u;
+    auto vec_vals = [&](u32x4 raw, uint32_t mw, uint32_t e0, float* v) {
         if (MASK) {
-            const uint32_t mb = mw >> (e0 & 31u);
+            const u32x4 m = SL.xt[(~mw >> (e0 & 31u)) & EMASK];
 #pragma unroll
-            for (int q = 0; q < EPV; ++q)
-                if (!((mb >> q) & 1u)) v[q] = -INFINITY;
+            for (int k = 0; k < 4; ++k) raw[k] = (m[k] & NINF) | (~m[k] & raw[k]);
         }
         if (special) {
             const uint32_t off0 = e0 - lo;
-            const uint32_t sk = L.spec[off0 >> 5] >> (off0 & 31u);
+            const u32x4 m = SL.xt[(L.spec[off0 >> 5] >> (off0 & 31u)) & EMASK];
 #pragma unroll
-            for (int q = 0; q < EPV; ++q)
-                if ((sk >> q) & 1u) v[q] = __builtin_nanf("");
+            for (int k = 0; k < 4; ++k) raw[k] |= m[k];
         }
+#pragma unroll
+        for (int q = 0; q < EPV; ++q) v[q] = unpack<DT>(raw, q);
     };
     // Per vector: its maximum decides everything.  The thread keeps the
     // lowest-id vector holding its running maximum; the element is resolved
@@ -1266,11 +1312,12 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
     uint32_t tj = NONE;  // first id of the best vector
     u32x4 traw = u32x4{0u, 0u, 0u, 0u};
     uint32_t tmw = 0xFFFFFFFFu;
-    auto process = [&](Tile<DT, TV, MASK>& T, uint32_t t0) {
+    auto process = [&](Tile<DT, TV, MASK>& T, uint32_t ch) {
+        const uint32_t t0 = chunk_t0(ch), sl = chunk_slot(ch);
 #pragma unroll
         for (int j = 0; j < TV; ++j) {
             asm volatile("" : "+v"(T.raw[j]));
-            const uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+            const uint32_t e0 = t0 + ((uint32_t)j * NT + sl) * EPV;
             const uint32_t mw = MASK ? T.mw[j] : 0xFFFFFFFFu;
             float v[EPV];
             vec_vals(T.raw[j], mw, e0, v);
@@ -1307,14 +1354,18 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
 #pragma unroll
                 for (int q = 0; q < EPV; ++q) gsum_add(v[q]);
             }
+            // one vector at a time: interleaving them only raises register
+            // pressure (the other waves hide the latencies)
+            __builtin_amdgcn_sched_barrier(0);
         }
     };
     // maximum of a tile (seeds the gather bound)
-    auto tile_max = [&](Tile<DT, TV, MASK>& T, uint32_t t0) {
+    auto tile_max = [&](Tile<DT, TV, MASK>& T, uint32_t ch) {
+        const uint32_t t0 = chunk_t0(ch), sl = chunk_slot(ch);
         float pm = -INFINITY;
 #pragma unroll
         for (int j = 0; j < TV; ++j) {
-            const uint32_t e0 = t0 + ((uint32_t)j * NT + tid) * EPV;
+            const uint32_t e0 = t0 + ((uint32_t)j * NT + sl) * EPV;
             float v[EPV];
             vec_vals(T.raw[j], MASK ? T.mw[j] : 0xFFFFFFFFu, e0, v);
             if (e0 < hi)
@@ -1325,62 +1376,52 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
     };
     // raises the wave's bound with its running maximum (no barrier)
     auto raise = [&]() {
-        mrun = fmaxf(mrun, wave_max(tm));
+        mrun = fmaxf(mrun, wave_max_dpp(tm));
         set_pre();
     };
 
+    // chunk 0..NW-1 (tile 0) seeds the gather bound with its block maximum:
+    // one barrier, then waves go alone; without a gather the barrier only
+    // publishes the chunk counter
     if (gather) {
-        // the first tile's block maximum: one barrier, then waves go alone
-        const float v = wave_max(tile_max(b0, tbase(0)));
+        const float v = wave_max_dpp(c0 < nchunk ? tile_max(b0, c0) : -INFINITY);
         if (lane == 0) SL.red[wv] = v;
-        __syncthreads();
+    }
+    __syncthreads();
+    if (gather) {
         float mm = SL.red[0];
 #pragma unroll
         for (int k = 1; k < NT / 64; ++k) mm = fmaxf(mm, SL.red[k]);
         mrun = mm;
         set_pre();
     }
-    // tile t of the (rotated) order: seed the bound if the wave has none yet,
-    // process, raise the bound
-    auto step = [&](Tile<DT, TV, MASK>& T, uint32_t t) __attribute__((always_inline)) {
-        if (gather && t > 0 && mrun == -INFINITY) {
-            mrun = wave_max(tile_max(T, tbase(t)));
+    // claims the next chunk for this wave
+    auto grab = [&]() {
+        uint32_t ch = 0;
+        if (lane == 0) ch = atomicAdd(&SL.next, 1u);
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)ch);
+    };
+    // process a chunk (seeding the bound first if the wave has none yet),
+    // claim the next one into the same buffer, raise the bound
+    auto step = [&](Tile<DT, TV, MASK>& T, uint32_t& ch) __attribute__((always_inline)) {
+        if (gather && mrun == -INFINITY) {
+            mrun = wave_max_dpp(tile_max(T, ch));
             set_pre();
         }
-        process(T, tbase(t));
-    };
-    // The steady-state loop refills both buffers unconditionally, so the
-    // compiler's wait for one buffer leaves the other's loads in flight; the
-    // last one to three tiles follow it.
-    auto stream = [&](auto fast_c) __attribute__((always_inline)) {
-        constexpr bool FAST = decltype(fast_c)::value;
-        auto load = [&](Tile<DT, TV, MASK>& T, uint32_t t) __attribute__((always_inline)) {
-            if (FAST) tile_load_fast<DT, TV, MASK, NT>(a, r, rp, tbase(t), hi, T);
-            else tile_load<DT, TV, MASK, NT>(a, r, rp, tbase(t), hi, T);
-        };
-        uint32_t t = 0;
-        for (; t + 3 < ntile; t += 2) {
-            step(b0, t);
-            load(b0, t + 2);
-            if (gather) raise();
-            step(b1, t + 1);
-            load(b1, t + 3);
-            if (gather) raise();
-        }
-        step(b0, t);
-        if (t + 2 < ntile) load(b0, t + 2);
+        process(T, ch);
+        ch = grab();
+        load(T, ch);
         if (gather) raise();
-        if (t + 1 < ntile) {
-            step(b1, t + 1);
-            if (gather) raise();
-        }
-        if (t + 2 < ntile) {
-            step(b0, t + 2);
-            if (gather) raise();
-        }
     };
-    if (fast) stream(std::true_type{});
-    else stream(std::false_type{});
+    // Both buffers are refilled unconditionally (a claim past the end loads a
+    // dummy line), so the compiler's wait for one buffer leaves the other's
+    // loads in flight.  Claims only grow: once one is past the end, so are
+    // all later ones.
+    while (c0 < nchunk) {
+        step(b0, c0);
+        if (c1 >= nchunk) break;
+        step(b1, c1);
+    }
     // the first element of the best vector that attains the maximum
     if (tj != NONE) {
         float v[EPV];
@@ -1595,16 +1636,6 @@ __device__ __forceinline__ Xd block_excl_scan_xd(Xd x, Xd* s_w) {
 }
 
 // first index i in [lo, hi) with S[i] >= t (S non-decreasing), hi if none
-__device__ __forceinline__ uint32_t first_ge(const float* S, uint32_t lo, uint32_t hi, float t) {
-    uint32_t a = lo, b = hi;
-    while (a < b) {
-        uint32_t mid = a + (b - a) / 2;
-        if (S[mid] >= t) b = mid;
-        else a = mid + 1;
-    }
-    return a;
-}
-
 __device__ __forceinline__ uint32_t bucket_of(uint64_t key) {
     uint32_t pb = (uint32_t)(key >> 32);
     uint32_t d = pb <= 0x3F800000u ? 0x3F800000u - pb : 0u;
@@ -2245,16 +2276,14 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
     pl.nch = (int)((vocab + pl.chunk - 1) / pl.chunk);
     // k_stream: enough (row, segment) workgroups to fill the GPU
     // (AXS_STREAM_WGS, default 1024: four per CU), segments a multiple of
-    // MIN_CHUNK ids and at most SEG_MAX; AXS_STREAM_TV picks the tile (4 or 8
-    // vectors per thread, default 4)
+    // MIN_CHUNK ids and at most SEG_MAX
     static const int target = env_int("AXS_STREAM_WGS", 1024);
-    static const int tv = env_int("AXS_STREAM_TV", 4) >= 8 ? 8 : 4;
     // enough rows to give every CU one: each row is one 1024-thread workgroup
     // that decides it in place (AXS_STREAM_WIDE_ROWS, default 240 rows)
     static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 240);
+    pl.tv = 4;
     if (nrows >= wide_rows && (uint32_t)vocab <= ROW_MAX) {
         pl.wide = true;
-        pl.tv = 4;
         pl.schunk = (uint32_t)vocab;
         pl.snch = 1;
         pl.vec = ((uintptr_t)base % 16 == 0) && ((stride * es) % 16 == 0) &&
@@ -2269,7 +2298,6 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
     if (seg > (int64_t)SEG_MAX) seg = SEG_MAX;
     pl.schunk = (uint32_t)seg;
     pl.snch = (int)(((int64_t)vocab + seg - 1) / seg);
-    pl.tv = tv;
     pl.vec = ((uintptr_t)base % 16 == 0) && ((stride * es) % 16 == 0) &&
              (base2 == nullptr || (uintptr_t)base2 % 16 == 0);
     return pl;
@@ -2302,19 +2330,26 @@ void launch_exact_mat(const Plan& pl, const KArgs& a, hipStream_t s) {
     }
 }
 
-template <int DT, int TV, int NT, uint32_t SEGMAX>
+template <int DT, int NT, uint32_t SEGMAX, bool FAST>
 void launch_stream_tv(const KArgs& a, hipStream_t s) {
     const int64_t total = (int64_t)a.nrows * a.snch;
     dim3 grid((unsigned)(((total + 7) / 8) * 8));
-    if (a.mask) hipLaunchKernelGGL((k_stream<DT, TV, true, NT, SEGMAX>), grid, dim3(NT), 0, s, a);
-    else hipLaunchKernelGGL((k_stream<DT, TV, false, NT, SEGMAX>), grid, dim3(NT), 0, s, a);
+    if (a.mask) hipLaunchKernelGGL((k_stream<DT, 4, true, NT, SEGMAX, FAST>), grid, dim3(NT), 0, s, a);
+    else hipLaunchKernelGGL((k_stream<DT, 4, false, NT, SEGMAX, FAST>), grid, dim3(NT), 0, s, a);
 }
 
+// fast: 16-byte aligned rows of whole vectors (every segment end, a multiple
+// of MIN_CHUNK or the vocabulary, is then a multiple of the vector width)
 template <int DT>
 void launch_stream_dt(const Plan& pl, const KArgs& a, hipStream_t s) {
-    if (pl.wide) launch_stream_tv<DT, 4, 1024, ROW_MAX>(a, s);
-    else if (pl.tv == 8) launch_stream_tv<DT, 8, NT_CHUNK, SEG_MAX>(a, s);
-    else launch_stream_tv<DT, 4, NT_CHUNK, SEG_MAX>(a, s);
+    const bool fast = a.vec && a.vocab % (DT == AXS_DTYPE_BF16 ? 8 : 4) == 0;
+    if (pl.wide) {
+        if (fast) launch_stream_tv<DT, 1024, ROW_MAX, true>(a, s);
+        else launch_stream_tv<DT, 1024, ROW_MAX, false>(a, s);
+    } else {
+        if (fast) launch_stream_tv<DT, NT_CHUNK, SEG_MAX, true>(a, s);
+        else launch_stream_tv<DT, NT_CHUNK, SEG_MAX, false>(a, s);
+    }
 }
 
 void launch_stream(const Plan& pl, const KArgs& a, hipStream_t s) {
