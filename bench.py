@@ -35,6 +35,20 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+def measured_traffic():
+    """HBM bytes per k_stream launch on this workload, from the committed
+    rocprofv3 FETCH_SIZE + WRITE_SIZE summary (copy-calibrated); None if absent."""
+    path = os.path.join(ROOT, "profiles", "k_stream_c3.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch"):
+                    return int(line.split("=")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(w, seconds=12.0, max_threads=16):
     """Times the CPU restatement of sample_categorical_into on f32 copies of the
     workload's rows (the reference samples host f32 logits after readback)."""
@@ -180,7 +194,9 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(),
+            "traffic_source": "profiles/k_stream_c3.md (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; "
+                              "scaled by a 256 MiB copy's readings)",
             "algorithmic_bytes": alg,
             "kernel_avg_us": round(chunk_us, 3),
             "step_GBps": round(step_gbs, 1),
