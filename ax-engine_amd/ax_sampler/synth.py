@@ -206,4 +206,99 @@ def make_c5(seed: int = 5, B: int = 32, depth: int = 3, V: int = 151936):
     return f32_to_bf16_bits(t), f32_to_bf16_bits(d), tp, dp
 
 
+def make_mixed(seed: int, B: int, V: int, dtype: int = DTYPE_BF16, hist_len: int = 512,
+               mask: bool = False, bias: bool = False, ngram: bool = False,
+               edge_rows: bool = True) -> Workload:
+    """Every row law at once, for parity tests of the routing and the edge cases.
+
+    Rows cycle through greedy, index-order (no filter), min-p only, min-p +
+    top-k + top-p, top-k, top-p, top_p <= 0 (sorted, untruncated) and a near-zero
+    temperature; penalties, window sizes and history lengths vary per row.
+    Optional: an allowed-token mask (densities 1%..100%, some rows all-allowed),
+    bias lists with duplicate ids and ids outside the vocabulary, and the
+    no-repeat n-gram ban.  With edge_rows, a few rows are all-equal, hold NaNs,
+    are all -inf but one id, or are all NaN."""
+    rng = np.random.default_rng([seed, 77, B, V])
+    noise = rng.standard_normal((B, V), dtype=np.float32) * np.float32(3.0)
+    if V >= 2:
+        head, top = _zipf_head(rng, B, V)
+    else:
+        head, top = np.zeros((B, V), np.float32), np.zeros((B, 64), np.uint32)
+    x = (noise + head).astype(np.float32)
+    if edge_rows and B >= 8:
+        x[1, :] = 1.5                       # all equal: every tie goes to the lowest id
+        x[2, rng.choice(V, max(1, V // 7), replace=False)] = np.nan
+        x[3, :] = -np.inf
+        x[3, V // 3] = 0.25
+        x[4, :] = np.nan
+        x[5, V - 1] = 60.0                  # maximum at the last id
+        x[6, 0] = 60.0                      # and at the first
+    logits = f32_to_bf16_bits(x) if dtype == DTYPE_BF16 else x
+    # histories of varied length (some empty), a quarter of the tokens hot
+    lens = rng.integers(0, hist_len + 1, size=B)
+    lens[::9] = 0
+    hs = []
+    for r in range(B):
+        h = rng.integers(0, V, size=lens[r], dtype=np.int64).astype(np.uint32)
+        pick = rng.random(lens[r]) < 0.25
+        h[pick] = top[r, rng.integers(0, 64, size=int(pick.sum()))]
+        hs.append(h)
+    off = np.zeros(B + 1, dtype=np.int64)
+    off[1:] = np.cumsum(lens)
+    hist = np.concatenate(hs).astype(np.uint32) if off[-1] else np.zeros(1, np.uint32)
+    p = _params(B)
+    laws = [
+        dict(temperature=0.0),
+        dict(temperature=0.8),
+        dict(temperature=0.9, has_min_p=1, min_p=0.05),
+        dict(temperature=1.0, has_min_p=1, min_p=0.02, top_k=64, top_p=0.95),
+        dict(temperature=0.7, top_k=40),
+        dict(temperature=1.1, top_p=0.9),
+        dict(temperature=0.6, top_p=0.0),
+        dict(temperature=1e-3, top_k=5, top_p=0.9),
+        dict(temperature=1.3, has_min_p=1, min_p=0.1, top_p=0.8),
+    ]
+    for r in range(B):
+        for k, v in laws[r % len(laws)].items():
+            p[r][k] = v
+    p["repetition_penalty"] = rng.choice(np.array([1.0, 1.05, 1.3, 0.8], np.float32), B)
+    p["presence_penalty"] = rng.choice(np.array([0.0, 0.5, -0.25], np.float32), B)
+    p["frequency_penalty"] = rng.choice(np.array([0.0, 0.3], np.float32), B)
+    ctx = rng.choice(np.array([AXS_NONE_U32, 16, 64, 0], np.uint32), B)
+    p["repetition_context_size"] = ctx
+    if ngram:
+        p["no_repeat_ngram_size"] = rng.choice(np.array([0, 2, 3], np.uint32), B)
+        p["ngram_window"] = rng.choice(np.array([32, 128, 1000], np.uint32), B)
+    p["seed"] = seed * 2654435761 + np.arange(B, dtype=np.uint64)
+    p["step"] = 13
+    w = Workload(f"mixed{B}x{V}", dtype, B, V, logits, p, hist, off)
+    if mask:
+        W = (V + 31) // 32
+        dens = rng.choice(np.array([0.01, 0.05, 0.3, 0.6, 1.0]), B)
+        allowed = rng.random((B, V)) < dens[:, None]
+        allowed[:, top[:, 0] % V] |= False
+        bits = np.zeros((B, W * 32), dtype=bool)
+        bits[:, :V] = allowed
+        w.mask = np.ascontiguousarray(np.packbits(bits, axis=1, bitorder="little").view("<u4"))
+        w.extra["allowed"] = allowed
+    if bias:
+        nb = rng.integers(0, 41, size=B)
+        ids, vals = [], []
+        for r in range(B):
+            t = rng.choice(top[r], size=nb[r] // 2).astype(np.int64)       # hot ids
+            u = rng.integers(0, V, size=nb[r] - nb[r] // 2, dtype=np.int64)
+            e = np.concatenate([t, u])
+            if nb[r] >= 4:
+                e[-1] = e[0]                      # a duplicate (applied twice, in order)
+                e[-2] = V + 5                     # outside the vocabulary (ignored)
+            ids.append(e.astype(np.uint32))
+            vals.append(rng.uniform(-6.0, 6.0, size=nb[r]).astype(np.float32))
+        boff = np.zeros(B + 1, dtype=np.int64)
+        boff[1:] = np.cumsum(nb)
+        w.bias_ids = np.concatenate(ids).astype(np.uint32) if boff[-1] else np.zeros(1, np.uint32)
+        w.bias_vals = np.concatenate(vals).astype(np.float32) if boff[-1] else np.zeros(1, np.float32)
+        w.bias_off = boff
+    return w
+
+
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4}

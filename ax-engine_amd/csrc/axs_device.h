@@ -144,6 +144,37 @@ __device__ __forceinline__ float wave_max_dpp(float x) {
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), 63));
 }
 
+// Unsigned minimum over the 64 lanes, the same DPP pattern; returned
+// wave-uniform.  Every lane must be active.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ uint32_t dpp_u(uint32_t x) {
+    return (uint32_t)__builtin_amdgcn_update_dpp((int)x, (int)x, CTRL, ROWS, 0xF, false);
+}
+__device__ __forceinline__ uint32_t wave_min_u32_dpp(uint32_t x) {
+    x = min(x, dpp_u<0xB1, 0xF>(x));
+    x = min(x, dpp_u<0x4E, 0xF>(x));
+    x = min(x, dpp_u<0x141, 0xF>(x));
+    x = min(x, dpp_u<0x140, 0xF>(x));
+    x = min(x, dpp_u<0x142, 0xA>(x));
+    x = min(x, dpp_u<0x143, 0xC>(x));
+    return (uint32_t)__builtin_amdgcn_readlane((int)x, 63);
+}
+
+// (value, index) argmax over the wave with the reference's rule (larger
+// value, then lower index; NONE never wins), wave-uniform result.  v is
+// never NaN.  Every lane must be active.
+__device__ __forceinline__ void wave_argmax_dpp(float& v, uint32_t& i) {
+    const float m = wave_max_dpp(i == NONE ? -INFINITY : v);
+    const uint32_t c = (i != NONE && v == m) ? i : NONE;
+    i = wave_min_u32_dpp(c);
+    v = m;
+}
+
+// exclusive count of the set bits of a 64-lane mask below this lane
+__device__ __forceinline__ uint32_t mbcnt64(uint64_t m) {
+    return __builtin_amdgcn_mbcnt_hi((uint32_t)(m >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)m, 0u));
+}
+
 __device__ __forceinline__ uint32_t wave_min_u32(uint32_t v) {
 #pragma unroll
     for (int d = 32; d > 0; d >>= 1) v = min(v, (uint32_t)__shfl_xor((int)v, d, 64));

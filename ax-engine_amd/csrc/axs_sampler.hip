@@ -882,6 +882,31 @@ __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_s
     }
 }
 
+// Lists row r for the exact path (second pass over its logits) with its
+// maximum m.  One thread.
+__device__ __forceinline__ void list_exact(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
+                                           uint32_t mode, bool sorted, uint32_t am) {
+    const bool minp = mode == M_MINP;
+    RowState rs;
+    rs.m = m;
+    rs.inv = inv;
+    rs.mode = mode;
+    rs.sorted = sorted ? 1u : 0u;
+    rs.ncompact = 0;
+    rs.minp_mg = __float_as_uint(INFINITY);
+    rs.amax = am;
+    rs.flags = 0;
+    rs.pmin = minp ? fmaxf(p.min_p, P_FLOOR) : P_FLOOR;
+    rs.u = row_uniform(a, r, p);
+    rs.kept = 0;
+    rs.F = 0.0f;
+    rs.nlist = 0;
+    rs.pad[0] = rs.pad[1] = rs.pad[2] = 0;
+    a.rstate[r] = rs;
+    const uint32_t idx = atomicAdd(a.exact_count, 1u);
+    a.exact_rows[idx] = (uint32_t)r;
+}
+
 // The row's decision from its merged statistics: the maximum m and its lowest
 // id am (NONE for an all-NaN row), the CS_* flags, gs = the sum of exp(l - m)
 // over finite l (greedy logprob), and cands(f), which calls f(id, l) for this
@@ -982,26 +1007,55 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
             if (tid < 64) decide_sorted<NT>(a, r, p, mode, sorted, F, n, flags0);
         }
     }
-    if (exact && tid == 0) {
-        RowState rs;
-        rs.m = m;
-        rs.inv = inv;
-        rs.mode = mode;
-        rs.sorted = sorted ? 1u : 0u;
-        rs.ncompact = 0;
-        rs.minp_mg = __float_as_uint(INFINITY);
-        rs.amax = am;
-        rs.flags = 0;
-        rs.pmin = minp ? fmaxf(p.min_p, P_FLOOR) : P_FLOOR;
-        rs.u = row_uniform(a, r, p);
-        rs.kept = 0;
-        rs.F = 0.0f;
-        rs.nlist = 0;
-        rs.pad[0] = rs.pad[1] = rs.pad[2] = 0;
-        a.rstate[r] = rs;
-        const uint32_t idx = atomicAdd(a.exact_count, 1u);
-        a.exact_rows[idx] = (uint32_t)r;
+    if (exact && tid == 0) list_exact(a, r, p, m, inv, mode, sorted, am);
+}
+
+// A min-p row decided by one wave from n <= 256 gathered candidates (a
+// superset of its min-p survivors, sampling.rs:283-294): survivors p =
+// exp((l - m) / T) >= min_p, ordered by (p desc, id asc) — or by id for an
+// index-order draw — with a bitonic sort in registers, then decide_sorted.
+// Called by the 64 lanes of one wave; no block barriers.
+template <int NT>
+__device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
+                                 uint32_t am, uint32_t n, const Cand* cand, FinLds<NT>& F) {
+    const int lane = threadIdx.x & 63;
+    const bool sorted = filters_enabled(p);
+    uint64_t k[4];
+    float mg = INFINITY;
+    uint32_t ns = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const uint32_t i = (uint32_t)lane + 64u * (uint32_t)j;
+        k[j] = 0ull;
+        bool keep = false;
+        if (i < n) {
+            const Cand cd = cand[i];
+            const float pr = prob_of(cd.l, m, inv);
+            mg = fminf(mg, fabsf(pr - p.min_p) / p.min_p);
+            keep = pr >= p.min_p;
+            if (keep) k[j] = sorted ? key_pdesc(pr, cd.id) : key_idasc(pr, cd.id);
+        }
+        ns += (uint32_t)__popcll(__ballot(keep));
     }
+    mg = -wave_max_dpp(-mg);
+    if (ns == 0) {  // (unreachable: the maximum itself has p = 1)
+        if (lane == 0) list_exact(a, r, p, m, inv, M_MINP, sorted, am);
+        return;
+    }
+    // survivors' keys are > 0, the empty slots 0: survivors come first
+    if (n <= 64) {
+        k[0] = wave_sort_desc(k[0]);
+        if ((uint32_t)lane < ns) F.key[lane] = k[0];
+    } else {
+        wave_sort_desc4(k);
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            if ((uint32_t)lane + 64u * (uint32_t)j < ns) F.key[lane + 64 * j] = k[j];
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    decide_sorted<NT>(a, r, p, M_MINP, sorted, F, ns, mg < 1e-6f ? AXS_FLAG_NEAR_MINP : 0u);
 }
 
 // Merges the published results of the nseg segments of row r and decides it.
@@ -1526,6 +1580,662 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
 }
 
 // --------------------------------------------------------------------------
+// k_row: one 1024-thread workgroup per row (large batches), the row decided
+// in place.  The logits stream starts at once: waves HWAVES.. issue their
+// first two chunks' loads before anything else, while waves 0..HWAVES-1 fetch
+// the repetition window first (their loads would otherwise queue behind the
+// tiles) and stage it in LDS.  The special-id tables are then
+//   spec  a bit per id: in the window, biased or banned
+//   hkey/hval  an open-addressing hash of the special ids: window count,
+//         bias entry, n-gram ban
+// The stream reads special elements as NaN (never a maximum, never a
+// candidate) and captures their raw values from its registers into the
+// wave's LDS region (a ballot gives each lane its slot: no atomics); after
+// the stream each captured element gets every processor from the hash and
+// joins the maximum and the candidates.  No scattered loads.  The row's
+// maximum is merged from per-wave DPP reductions, and a min-p row with at
+// most 256 candidates is decided by wave 0 alone (register bitonic sort, no
+// block barriers).
+// --------------------------------------------------------------------------
+constexpr int RT = 1024;               // threads of a row workgroup
+constexpr int RWV = RT / 64;           // its waves
+constexpr int HWAVES = 2;              // waves that fetch the window before their tiles
+constexpr uint32_t HPRE = 2048;        // window tokens staged through LDS
+constexpr uint32_t HBITS = 12;
+constexpr uint32_t HSZ = 1u << HBITS;  // hash slots
+constexpr uint32_t CAPW = 384;         // captured special elements per wave
+constexpr uint32_t RBCAP = 1024;       // bias entries per row
+constexpr uint32_t HV_CNT = 0x000FFFFFu;  // window count
+constexpr uint32_t HV_BSH = 20;           // bias entry index + 1, or HV_BMULTI
+constexpr uint32_t HV_BMULTI = 0x7FFu;
+constexpr uint32_t HV_BAN = 0x80000000u;
+constexpr uint32_t CAP_OFF = 0x80000000u;  // captured element is masked off
+constexpr uint32_t RERR_HASH = 1u;         // more special ids than hash slots
+constexpr uint32_t RERR_BIAS = 2u;         // more bias entries than RBCAP
+constexpr uint32_t RERR_CAP = 4u;          // a wave captured more than CAPW
+
+struct RowLds {
+    union {
+        struct {
+            uint32_t spec[ROW_MAX / 32];
+            uint32_t hkey[HSZ];
+            uint32_t hval[HSZ];
+        } p;
+        FinLds<RT> F;
+    } u;
+    union {
+        uint32_t stage[HPRE];
+        Cand cand[FIN_CAP];
+    } v;
+    Cand cap[RWV][CAPW];
+    uint32_t bias_id[RBCAP];
+    float bias_v[RBCAP];
+    u32x4 xt[256];
+    float wm[RWV];      // per-wave maximum ...
+    uint32_t wa[RWV];   // ... and its lowest id
+    float gm[RWV];      // per-wave greedy logprob partials: maximum ...
+    float gs[RWV];      // ... and sum of exp(l - maximum)
+    uint32_t ncand, next, nbias, err;
+    uint32_t bpos;  // some bias entry is not <= 0 (it may raise a logit)
+    int gmax;       // shared lower bound of the row maximum (ordered-int encoding)
+};
+
+__device__ __forceinline__ int f2ord(float f) {
+    const int k = __float_as_int(f);
+    return k >= 0 ? k : k ^ 0x7FFFFFFF;
+}
+__device__ __forceinline__ float ord2f(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF); }
+
+// home slot of id t: the murmur3 finalizer, so that arithmetic progressions
+// of ids (a permuted vocabulary's top ranks, for one) do not cluster
+__device__ __forceinline__ uint32_t hslot0(uint32_t t) {
+    t ^= t >> 16;
+    t *= 0x85EBCA6Bu;
+    t ^= t >> 13;
+    t *= 0xC2B2AE35u;
+    t ^= t >> 16;
+    return t & (HSZ - 1u);
+}
+
+// slot of special id t, inserting it if absent; NONE when HPROBE slots from
+// its home are taken by other ids (the row then resolves its special ids
+// from HBM)
+constexpr uint32_t HPROBE = 256;
+__device__ __forceinline__ uint32_t hash_insert(uint32_t* hkey, uint32_t t) {
+    uint32_t h = hslot0(t);
+    for (uint32_t k = 0; k < HPROBE; ++k) {
+        const uint32_t old = atomicCAS(&hkey[h], NONE, t);
+        if (old == NONE || old == t) return h;
+        h = (h + 1u) & (HSZ - 1u);
+    }
+    return NONE;
+}
+
+// slot of special id t (present by construction unless an insert failed)
+__device__ __forceinline__ uint32_t hash_find(const uint32_t* hkey, uint32_t t) {
+    uint32_t h = hslot0(t);
+    for (uint32_t k = 0; k < HPROBE; ++k) {
+        const uint32_t key = hkey[h];
+        if (key == t) return h;
+        if (key == NONE) return NONE;
+        h = (h + 1u) & (HSZ - 1u);
+    }
+    return NONE;
+}
+
+// Every processor in order for special id e with raw logit l: repetition →
+// presence/frequency → bias → mask → n-gram ban (sampling.rs:875-920 for the
+// first and last; the others are this build's extensions).  cnt is the id's
+// window count, bcode its bias entry (index + 1, 0 for none, HV_BMULTI for
+// several), off whether the mask disallows it.
+__device__ __forceinline__ float row_special_value(const RowCtx& c, const RowLds& SL, uint32_t e, float l,
+                                                  uint32_t cnt, uint32_t bcode, bool ban, bool off) {
+    if (c.cnt_on && cnt) {
+        if (c.rep_on) {
+            const float rep = c.p.repetition_penalty;
+            l = l < 0.0f ? __fmul_rn(l, rep) : __fdiv_rn(l, rep);
+        }
+        if (c.pf_on) {
+            l = __fsub_rn(l, __fmul_rn(c.p.frequency_penalty, (float)cnt));
+            l = __fsub_rn(l, c.p.presence_penalty);
+        }
+    }
+    if (c.bias_on) {
+        if (bcode == HV_BMULTI) {
+            // several entries for this id: added one by one in list order
+            for (uint32_t j = 0; j < SL.nbias; ++j)
+                if (SL.bias_id[j] == e) l = __fadd_rn(l, SL.bias_v[j]);
+        } else if (bcode) {
+            l = __fadd_rn(l, SL.bias_v[bcode - 1u]);
+        }
+    }
+    if (off) l = -INFINITY;
+    if (ban) l = -INFINITY;
+    return l;
+}
+
+template <int DT, int TV, bool MASK, bool FAST>
+__global__ __launch_bounds__(RT) void k_row(KArgs a) {
+    constexpr int EPV = Ev<DT>::EPV;
+    constexpr uint32_t TILE = (uint32_t)RT * TV * EPV;
+    constexpr uint32_t NW = RWV;
+    __shared__ RowLds SL;
+    const int tid = threadIdx.x;
+    const int wv = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int lane = tid & 63;
+    const int64_t w = xcd_item(a.nrows);
+    if (w >= a.nrows) return;
+    const int r = (int)w;
+    const uint32_t lo = 0u, hi = (uint32_t)a.vocab;
+    const uint32_t ntile = (hi + TILE - 1) / TILE;
+    const char* rp = row_ptr(a, r);
+    // rows start at different tiles so they do not all read the same HBM
+    // channels at once (the order of visits does not matter: ties are broken
+    // by id)
+    const uint32_t rot = (uint32_t)(((uint64_t)w * 5u) % ntile);
+    auto tbase = [&](uint32_t k) {
+        uint32_t t = k + rot;
+        if (t >= ntile) t -= ntile;
+        return t * TILE;
+    };
+    // chunk ch = one wave's share of a tile: slot ch % NW of tile ch / NW
+    const uint32_t nchunk = ntile * NW;
+    auto chunk_t0 = [&](uint32_t ch) { return tbase(ch / NW); };
+    auto chunk_slot = [&](uint32_t ch) { return (ch % NW) * 64u + (uint32_t)lane; };
+    auto load = [&](Tile<DT, TV, MASK>& T, uint32_t ch) __attribute__((always_inline)) {
+        const bool valid = ch < nchunk;  // wave-uniform
+        if (FAST) {
+            tile_load_fast<DT, TV, MASK, RT>(a, r, rp, valid ? chunk_t0(ch) : lo, hi, valid ? chunk_slot(ch) : 0u,
+                                             valid, T);
+        } else {
+            const uint32_t t0 = valid ? chunk_t0(ch) : lo;
+            tile_load<DT, TV, MASK, RT>(a, r, rp, t0, valid ? hi : t0, valid ? chunk_slot(ch) : 0u, T);
+        }
+    };
+    uint32_t c0 = (uint32_t)wv, c1 = NW + (uint32_t)wv;
+    Tile<DT, TV, MASK> b0, b1;
+    if (wv >= HWAVES) {
+        load(b0, c0);
+        load(b1, c1);
+    }
+    const RowCtx c = make_ctx(a, r);
+    const bool special = c.cnt_on || c.bias_on || c.ban_on;
+    // the window's first HPRE tokens (waves 0..HWAVES-1, ahead of their tiles)
+    constexpr int HK = (int)(HPRE / (HWAVES * 64));
+    uint32_t ht[HK];
+    if (wv < HWAVES) {
+#pragma unroll
+        for (int k = 0; k < HK; ++k) {
+            const int64_t i = c.w0 + tid + (int64_t)k * (HWAVES * 64);
+            ht[k] = (c.cnt_on && i < c.w1) ? a.hist[i] : NONE;
+        }
+        load(b0, c0);
+        load(b1, c1);
+    }
+    if (tid == 0) {
+        SL.next = 2u * NW;
+        SL.ncand = 0;
+        SL.err = 0;
+        SL.bpos = 0;
+        SL.gmax = f2ord(-INFINITY);
+        const int64_t nb = c.bias_on ? c.b1 - c.b0 : 0;
+        SL.nbias = (uint32_t)(nb < (int64_t)RBCAP ? nb : (int64_t)RBCAP);
+    }
+    if (special || MASK) {
+        // expansion table: bit q of an index marks element q of a vector; the
+        // entry holds, per 32-bit word of the vector, all ones over the
+        // marked elements
+        for (uint32_t i = tid; i < 256u; i += RT) {
+            u32x4 m;
+#pragma unroll
+            for (int k = 0; k < 4; ++k) {
+                if (DT == AXS_DTYPE_BF16)
+                    m[k] = (((i >> (2 * k)) & 1u) ? 0x0000FFFFu : 0u) | (((i >> (2 * k + 1)) & 1u) ? 0xFFFF0000u : 0u);
+                else
+                    m[k] = ((i >> k) & 1u) ? 0xFFFFFFFFu : 0u;
+            }
+            SL.xt[i] = m;
+        }
+    }
+    if (special) {
+        const uint32_t nw = (hi + 31u) / 32u;
+        for (uint32_t i = tid; i < nw; i += RT) SL.u.p.spec[i] = 0u;
+        for (uint32_t i = tid; i < HSZ; i += RT) {
+            SL.u.p.hkey[i] = NONE;
+            SL.u.p.hval[i] = 0u;
+        }
+        if (c.bias_on) {
+            bool pos = false;
+            for (int64_t i = c.b0 + tid; i < c.b1 && i < c.b0 + (int64_t)RBCAP; i += RT) {
+                SL.bias_id[i - c.b0] = a.bias_ids[i];
+                const float bv = a.bias_vals[i];
+                SL.bias_v[i - c.b0] = bv;
+                pos |= !(bv <= 0.0f);
+            }
+            if (pos) SL.bpos = 1u;
+        }
+        if (wv < HWAVES) {
+#pragma unroll
+            for (int k = 0; k < HK; ++k) SL.v.stage[tid + k * (HWAVES * 64)] = ht[k];
+        }
+    }
+    __syncthreads();
+    if (special) {
+        uint32_t* spec = SL.u.p.spec;
+        uint32_t* hkey = SL.u.p.hkey;
+        uint32_t* hval = SL.u.p.hval;
+        auto mark = [&](uint32_t t) { atomicOr(&spec[t >> 5], 1u << (t & 31u)); };
+        bool full = false;
+        auto count = [&](uint32_t t) {
+            if (t >= hi) return;  // ids outside the vocabulary are skipped
+            mark(t);              // (the bitmap is always complete)
+            if (full) return;
+            const uint32_t s = hash_insert(hkey, t);
+            if (s == NONE) full = true;
+            else atomicAdd(&hval[s], 1u);
+        };
+        if (c.cnt_on) {
+            if (c.w1 - c.w0 > (int64_t)HV_CNT) full = true;  // counts would not fit
+#pragma unroll
+            for (int k = 0; k < (int)(HPRE / RT); ++k) {
+                const uint32_t t = SL.v.stage[tid + k * RT];
+                if (t != NONE) count(t);
+            }
+            for (int64_t i = c.w0 + HPRE + tid; i < c.w1; i += RT) count(a.hist[i]);
+        }
+        if (c.bias_on) {
+            if (c.b1 - c.b0 > (int64_t)RBCAP) {
+                if (tid == 0) SL.err |= RERR_BIAS;
+            }
+            for (uint32_t j = tid; j < SL.nbias; j += RT) {
+                const uint32_t t = SL.bias_id[j];
+                if (t >= hi) continue;
+                mark(t);
+                const uint32_t s = hash_insert(hkey, t);
+                if (s == NONE) {
+                    full = true;
+                    continue;
+                }
+                uint32_t old = hval[s];
+                while (true) {
+                    const uint32_t b = (old >> HV_BSH) & HV_BMULTI;
+                    const uint32_t nb = b == 0u ? j + 1u : HV_BMULTI;
+                    const uint32_t nv = (old & ~(HV_BMULTI << HV_BSH)) | (nb << HV_BSH);
+                    const uint32_t got = atomicCAS(&hval[s], old, nv);
+                    if (got == old) break;
+                    old = got;
+                }
+            }
+        }
+        if (c.ban_on)
+            ngram_each<RT>(a, c, lo, hi, [&](uint32_t t) {
+                mark(t);
+                const uint32_t s = hash_insert(hkey, t);
+                if (s == NONE) full = true;
+                else atomicOr(&hval[s], HV_BAN);
+            });
+        if (full) atomicOr(&SL.err, RERR_HASH);
+        __syncthreads();
+    }
+    const bool hfull = special && (SL.err & RERR_HASH);
+
+    const uint32_t mode = c.mode;
+    const float inv = __fdiv_rn(1.0f, c.p.temperature);
+    const bool gather = mode == M_MINP && isfinite(inv);
+    const bool gsum_on = mode == M_GREEDY && a.want_logprob;
+    const float thr = gather ? __fsub_rn(ln_f32(c.p.min_p), 1e-3f) : 0.0f;
+    const uint32_t sflags = (c.err || (SL.err & RERR_BIAS)) ? CS_ERROR : 0u;
+    // Processors that can only lower a logit (repetition >= 1, presence and
+    // frequency >= 0, biases <= 0, mask, ban) let the stream skip every
+    // vector whose raw maximum is below rthr: none of its plain elements can
+    // be the maximum or a min-p candidate, and none of its special ones either
+    // (processed <= raw).  Otherwise, and for the greedy logprob sum, every
+    // vector is looked at.
+    const bool mono = (!c.rep_on || c.p.repetition_penalty > 1.0f) &&
+                      (!c.pf_on || (c.p.presence_penalty >= 0.0f && c.p.frequency_penalty >= 0.0f)) &&
+                      (!c.bias_on || SL.bpos == 0u);
+    const bool fastp = mono && !gsum_on;
+    const double dlow = gather ? ((double)thr - 0.01) / (double)inv : 0.0;
+
+    float tm = -INFINITY;             // thread maximum (non-special ids)
+    uint32_t ta = NONE;               // its lowest id
+    float gm = -INFINITY, gs = 0.0f;  // greedy logprob: sum of exp(l - gm)
+    float mrun = -INFINITY;           // a lower bound of the row maximum (wave-uniform)
+    float lpre = INFINITY;            // l < lpre ⇒ not a candidate (wave-uniform)
+    float rthr = -INFINITY;           // raw vector maximum < rthr ⇒ skipped (wave-uniform)
+
+    auto set_pre = [&]() {
+        // (l - mrun) * inv >= thr needs l >= mrun + thr / inv; the bound is
+        // lowered by 0.01 nats and a few ulps so rounding never excludes one
+        if (gather) {
+            if (!isfinite(mrun)) {
+                lpre = INFINITY;
+            } else if (inv > 0.0f) {
+                const double bnd = (double)mrun + dlow;
+                const double slack = 4.0 * fmax(fabs((double)mrun), fabs(bnd)) * 1.2e-7;
+                lpre = (float)(bnd - slack);
+            } else {
+                lpre = -INFINITY;
+            }
+        }
+        rthr = !fastp ? -INFINITY : (gather ? fminf(lpre, mrun) : mrun);
+    };
+    auto add_cand = [&](uint32_t e, float l) {
+        const uint32_t slot = atomicAdd(&SL.ncand, 1u);
+        if (slot < FIN_CAP) {
+            SL.v.cand[slot].id = e;
+            SL.v.cand[slot].l = l;
+        }
+    };
+    auto gsum_add = [&](float l) {
+        if (isfinite(l)) {
+            if (l > gm) {
+                gs = __fmaf_rn(gs, __expf(gm - l), 1.0f);
+                gm = l;
+            } else {
+                gs += __expf(l - gm);
+            }
+        }
+    };
+    constexpr uint32_t EMASK = (1u << EPV) - 1u;
+    constexpr uint32_t NINF = DT == AXS_DTYPE_BF16 ? 0xFF80FF80u : 0xFF800000u;
+    // The special bits of the vector at e0
+    auto spec_bits = [&](uint32_t e0) -> uint32_t {
+        return special ? (SL.u.p.spec[e0 >> 5] >> (e0 & 31u)) & EMASK : 0u;
+    };
+    // The EPV logits of a vector as the stream sees them: disallowed elements
+    // -inf, special ones (bits sk) NaN (an all-ones pattern in both formats)
+    auto vec_vals = [&](u32x4 raw, uint32_t mw, uint32_t e0, uint32_t sk, float* v) {
+        if (MASK) {
+            const u32x4 m = SL.xt[(~mw >> (e0 & 31u)) & EMASK];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) raw[k] = (m[k] & NINF) | (~m[k] & raw[k]);
+        }
+        if (special) {
+            const u32x4 m = SL.xt[sk];
+#pragma unroll
+            for (int k = 0; k < 4; ++k) raw[k] |= m[k];
+        }
+#pragma unroll
+        for (int q = 0; q < EPV; ++q) v[q] = unpack<DT>(raw, q);
+    };
+    // element q (lane-varying) of a vector, as f32
+    auto elem = [&](const u32x4& raw, uint32_t q) -> float {
+        if (DT == AXS_DTYPE_BF16) {
+            const uint32_t wi = q >> 1;
+            const uint32_t lo = (wi & 1u) ? raw[1] : raw[0];
+            const uint32_t hi2 = (wi & 1u) ? raw[3] : raw[2];
+            const uint32_t w = (wi & 2u) ? hi2 : lo;
+            return __uint_as_float((q & 1u) ? (w & 0xFFFF0000u) : (w << 16));
+        } else {
+            const uint32_t lo = (q & 1u) ? raw[1] : raw[0];
+            const uint32_t hi2 = (q & 1u) ? raw[3] : raw[2];
+            return __uint_as_float((q & 2u) ? hi2 : lo);
+        }
+    };
+    // The wave's lanes holding special elements (bits sk) append (id, raw
+    // value) to the wave's capture region; wcnt is the wave's running count.
+    Cand* capw = SL.cap[wv];
+    uint32_t wcnt = 0;
+    auto capture = [&](const u32x4& raw, uint32_t mw, uint32_t e0, uint32_t sk) {
+        const uint64_t m1 = __ballot(sk != 0u);
+        if (m1 == 0ull) return;
+        const uint64_t m2 = __ballot((sk & (sk - 1u)) != 0u);
+        if (m2 == 0ull) {
+            // at most one special element per lane (the common case)
+            const uint32_t pos = wcnt + mbcnt64(m1);
+            if (sk != 0u && pos < CAPW) {
+                const uint32_t q = (uint32_t)__ffs((int)sk) - 1u;
+                const bool off = MASK && !((mw >> ((e0 + q) & 31u)) & 1u);
+                capw[pos].id = (e0 + q) | (off ? CAP_OFF : 0u);
+                capw[pos].l = elem(raw, q);
+            }
+            wcnt += (uint32_t)__popcll(m1);
+        } else {
+            // per-lane counts up to EPV: prefix from their bit slices
+            const uint32_t c = (uint32_t)__popc(sk);
+            uint32_t pre = 0, tot = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint64_t mb = __ballot((c >> b) & 1u);
+                pre += mbcnt64(mb) << b;
+                tot += (uint32_t)__popcll(mb) << b;
+            }
+            uint32_t pos = wcnt + pre;
+#pragma unroll
+            for (int q = 0; q < EPV; ++q)
+                if ((sk >> q) & 1u) {
+                    if (pos < CAPW) {
+                        const bool off = MASK && !((mw >> ((e0 + q) & 31u)) & 1u);
+                        capw[pos].id = (e0 + q) | (off ? CAP_OFF : 0u);
+                        capw[pos].l = unpack<DT>(raw, q);
+                    }
+                    ++pos;
+                }
+            wcnt += tot;
+        }
+    };
+    // Per vector: its maximum decides everything.  The thread keeps the
+    // lowest-id vector holding its running maximum; the element is resolved
+    // once at the end.  Only vectors reaching the gather bound, and greedy
+    // rows that want a logprob, look at single elements.
+    uint32_t tj = NONE;  // first id of the best vector
+    u32x4 traw = u32x4{0u, 0u, 0u, 0u};
+    uint32_t tmw = 0xFFFFFFFFu;
+    // The full look at one vector with special bits sk: special elements
+    // read as NaN, disallowed ones -inf; the lane's maximum, min-p candidates
+    // and the greedy logprob sum updated.  Runs with only the relevant lanes
+    // active (the capture, whose ballots need the whole wave, is done before).
+    auto look = [&](const u32x4& raw, uint32_t mw, uint32_t e0, uint32_t sk) __attribute__((always_inline)) {
+        float v[EPV];
+        vec_vals(raw, mw, e0, sk, v);
+        float vm = v[0];
+#pragma unroll
+        for (int q = 1; q < EPV; ++q) vm = fmaxf(vm, v[q]);
+        if (vm > tm || (vm == tm && e0 < tj)) {
+            tm = vm;
+            tj = e0;
+            traw = raw;
+            tmw = mw;
+        }
+        if (gather && vm >= lpre) {
+            // one slot reservation for all of the vector's candidates
+            uint32_t qm = 0;
+#pragma unroll
+            for (int q = 0; q < EPV; ++q)
+                if (v[q] >= lpre && __fmul_rn(__fsub_rn(v[q], mrun), inv) >= thr) qm |= 1u << q;
+            if (qm) {
+                uint32_t slot = atomicAdd(&SL.ncand, (uint32_t)__popc(qm));
+#pragma unroll
+                for (int q = 0; q < EPV; ++q)
+                    if ((qm >> q) & 1u) {
+                        if (slot < FIN_CAP) {
+                            SL.v.cand[slot].id = e0 + q;
+                            SL.v.cand[slot].l = v[q];
+                        }
+                        ++slot;
+                    }
+            }
+        }
+        if (gsum_on) {
+#pragma unroll
+            for (int q = 0; q < EPV; ++q) gsum_add(v[q]);
+        }
+    };
+    // Per vector: its raw maximum (special and disallowed elements included)
+    // against rthr; the wave looks closer only when some lane reaches it.
+    auto process = [&](Tile<DT, TV, MASK>& T, uint32_t ch) {
+        const uint32_t t0 = chunk_t0(ch), sl = chunk_slot(ch);
+#pragma unroll
+        for (int j = 0; j < TV; ++j) {
+            asm volatile("" : "+v"(T.raw[j]));
+            const uint32_t e0 = t0 + ((uint32_t)j * RT + sl) * EPV;
+            const uint32_t mw = MASK ? T.mw[j] : 0xFFFFFFFFu;
+            const bool in = e0 < hi;  // lanes past the row end re-read a vector
+            float vr = unpack<DT>(T.raw[j], 0);
+#pragma unroll
+            for (int q = 1; q < EPV; ++q) vr = fmaxf(vr, unpack<DT>(T.raw[j], q));
+            // (an all-NaN vector is looked at: masked or banned, NaN is -inf)
+            const bool rel = in && !(vr < rthr);
+            if (__ballot(rel) != 0ull) {
+                // whole wave: the capture keeps a wave-uniform count
+                const uint32_t sk = rel ? spec_bits(e0) : 0u;
+                if (special) capture(T.raw[j], mw, e0, sk);
+                if (rel) look(T.raw[j], mw, e0, sk);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // maximum of a chunk (seeds a wave's gather bound)
+    auto tile_max = [&](Tile<DT, TV, MASK>& T, uint32_t ch) {
+        const uint32_t t0 = chunk_t0(ch), sl = chunk_slot(ch);
+        float pm = -INFINITY;
+#pragma unroll
+        for (int j = 0; j < TV; ++j) {
+            const uint32_t e0 = t0 + ((uint32_t)j * RT + sl) * EPV;
+            float v[EPV];
+            vec_vals(T.raw[j], MASK ? T.mw[j] : 0xFFFFFFFFu, e0, spec_bits(e0), v);
+            if (e0 < hi)
+#pragma unroll
+                for (int q = 0; q < EPV; ++q) pm = fmaxf(pm, v[q]);
+        }
+        return pm;
+    };
+    // raises the wave's bound: its own maximum, shared through SL.gmax
+    auto raise = [&](float wm) {
+        int g = 0;
+        if (lane == 0) g = atomicMax(&SL.gmax, f2ord(wm));
+        g = __builtin_amdgcn_readfirstlane(g);
+        mrun = fmaxf(mrun, fmaxf(wm, ord2f(g)));
+        set_pre();
+    };
+    auto grab = [&]() {
+        uint32_t ch = 0;
+        if (lane == 0) ch = atomicAdd(&SL.next, 1u);
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)ch);
+    };
+    const bool bound = gather || fastp;  // the stream keeps a lower bound of the maximum
+    auto step = [&](Tile<DT, TV, MASK>& T, uint32_t& ch) __attribute__((always_inline)) {
+        if (bound && mrun == -INFINITY) raise(wave_max_dpp(tile_max(T, ch)));
+        process(T, ch);
+        ch = grab();
+        load(T, ch);
+        if (bound) raise(wave_max_dpp(tm));
+    };
+    // Both buffers are refilled unconditionally (a claim past the end loads a
+    // dummy line), so the wait for one buffer leaves the other's loads in
+    // flight.  Claims only grow: once one is past the end, so are all later.
+    while (c0 < nchunk) {
+        step(b0, c0);
+        if (c1 >= nchunk) break;
+        step(b1, c1);
+    }
+    // the first element of the best vector that attains the maximum
+    if (tj != NONE) {
+        float v[EPV];
+        vec_vals(traw, tmw, tj, spec_bits(tj), v);
+        uint32_t q0 = NONE;
+#pragma unroll
+        for (int q = EPV - 1; q >= 0; --q)
+            if (v[q] == tm) q0 = (uint32_t)q;
+        ta = tj + q0;
+    }
+    if (special && lane == 0 && wcnt > CAPW) atomicOr(&SL.err, RERR_CAP);
+    __syncthreads();
+    // the special ids' processed values
+    if (special) {
+        auto visit = [&](uint32_t e, float l) {
+            am_merge(tm, ta, l, isnan(l) ? NONE : e);
+            if (gather && l > -INFINITY && (mrun == -INFINITY || __fmul_rn(__fsub_rn(l, mrun), inv) >= thr))
+                add_cand(e, l);
+            if (gsum_on) gsum_add(l);
+        };
+        if (!(SL.err & (RERR_HASH | RERR_CAP))) {
+            // each wave its own captures
+            for (uint32_t i = (uint32_t)lane; i < wcnt; i += 64u) {
+                const Cand cd = capw[i];
+                const uint32_t e = cd.id & ~CAP_OFF;
+                const uint32_t s = hash_find(SL.u.p.hkey, e);
+                const uint32_t hv = s == NONE ? 0u : SL.u.p.hval[s];
+                visit(e, row_special_value(c, SL, e, cd.l, hv & HV_CNT, (hv >> HV_BSH) & HV_BMULTI,
+                                           (hv & HV_BAN) != 0u, (cd.id & CAP_OFF) != 0u));
+            }
+        } else {
+            // a full hash or capture region: every special id resolved from
+            // HBM (raw logit; window count and ban from the hash, or, when it
+            // is full, by scanning the history)
+            const bool hok = !(SL.err & RERR_HASH);
+            const uint32_t nw = (hi + 31u) / 32u;
+            for (uint32_t wi = tid; wi < nw; wi += RT) {
+                uint32_t bits = SL.u.p.spec[wi];
+                while (bits) {
+                    const uint32_t b = (uint32_t)__ffs((int)bits) - 1u;
+                    bits &= bits - 1u;
+                    const uint32_t e = wi * 32u + b;
+                    uint32_t cnt, bcode;
+                    bool ban;
+                    if (hok) {
+                        const uint32_t s = hash_find(SL.u.p.hkey, e);
+                        const uint32_t hv = s == NONE ? 0u : SL.u.p.hval[s];
+                        cnt = hv & HV_CNT;
+                        bcode = (hv >> HV_BSH) & HV_BMULTI;
+                        ban = (hv & HV_BAN) != 0u;
+                    } else {
+                        const uint32_t cw = count_word_hbm(a, c, e);
+                        cnt = cw & ~CNT_BAN;
+                        bcode = HV_BMULTI;
+                        ban = (cw & CNT_BAN) != 0u;
+                    }
+                    const bool off = c.mask_on && !((a.mask[(size_t)r * a.mask_stride + (e >> 5)] >> (e & 31u)) & 1u);
+                    visit(e, row_special_value(c, SL, e, raw_at<DT>(rp, e), cnt, bcode, ban, off));
+                }
+            }
+        }
+    }
+
+    // row results: per-wave DPP reductions, merged by every thread
+    float bm = tm;
+    uint32_t bi = ta;
+    wave_argmax_dpp(bm, bi);
+    float wgm = -INFINITY, wgs = 0.0f;
+    if (gsum_on) {
+        wgm = wave_max_dpp(gm);
+        const float part = (isfinite(gm) && isfinite(wgm)) ? gs * __expf(gm - wgm) : 0.0f;
+        wgs = wave_sum_f(part);
+    }
+    if (lane == 0) {
+        SL.wm[wv] = bm;
+        SL.wa[wv] = bi;
+        SL.gm[wv] = wgm;
+        SL.gs[wv] = wgs;
+    }
+    __syncthreads();
+    float m = SL.wm[0];
+    uint32_t am = SL.wa[0];
+#pragma unroll
+    for (int k = 1; k < RWV; ++k) am_merge(m, am, SL.wm[k], SL.wa[k]);
+    if (am == NONE) m = -INFINITY;
+    double gsum = 0.0;
+    if (gsum_on && isfinite(m)) {
+#pragma unroll
+        for (int k = 0; k < RWV; ++k)
+            if (isfinite(SL.gm[k])) gsum += (double)SL.gs[k] * exp((double)SL.gm[k] - (double)m);
+    }
+    uint32_t flags = sflags;
+    const uint32_t n = gather ? SL.ncand : 0u;
+    if (gather && n > FIN_CAP) flags |= CS_OVERFLOW;
+    if (gather && !(flags & (CS_ERROR | CS_OVERFLOW)) && am != NONE && isfinite(m) && n <= 256u) {
+        // min-p row with few candidates: wave 0 decides alone
+        if (wv != 0) return;
+        wave_decide_minp<RT>(a, r, c.p, m, inv, am, n, SL.v.cand, SL.u.F);
+        return;
+    }
+    finish_decide<RT>(a, r, c.p, m, am, flags, gsum, n, SL.u.F, [&](auto&& f) {
+        for (uint32_t i = tid; i < n; i += RT) f(SL.v.cand[i].id, SL.v.cand[i].l);
+    });
+}
+
+// --------------------------------------------------------------------------
 // k_exact_mat: exact probabilities of the listed rows (second pass)
 // --------------------------------------------------------------------------
 template <int DT, int NV>
@@ -1915,8 +2625,13 @@ __device__ void exact_row(const KArgs& a) {
     if (a.out_kept && a.out_kept_cap > 0) {
         uint32_t cap = (uint32_t)a.out_kept_cap;
         if (sorted) {
+            // kept entries below the compaction floor (p < 2^-24 of the
+            // maximum's: never drawn) are not ordered here; they are listed
+            // as NONE after the ordered prefix
             uint32_t nw = Lk < cap ? Lk : cap;
             for (uint32_t i = 0; i < nw; ++i) a.out_kept[(size_t)r * cap + i] = pdesc_id(keys[i]);
+            const uint32_t ne = kept < cap ? kept : cap;
+            for (uint32_t i = nw; i < ne; ++i) a.out_kept[(size_t)r * cap + i] = NONE;
         }
     }
     if (a.ws_kept_id) {
@@ -2338,14 +3053,29 @@ void launch_stream_tv(const KArgs& a, hipStream_t s) {
     else hipLaunchKernelGGL((k_stream<DT, 4, false, NT, SEGMAX, FAST>), grid, dim3(NT), 0, s, a);
 }
 
+// one row per 1024-thread workgroup; AXS_ROW_TV (4 or 8, tuning) vectors per
+// lane in each chunk
+template <int DT, bool FAST, int TV>
+void launch_row_tv(const KArgs& a, hipStream_t s) {
+    dim3 grid((unsigned)(((a.nrows + 7) / 8) * 8));
+    if (a.mask) hipLaunchKernelGGL((k_row<DT, TV, true, FAST>), grid, dim3(RT), 0, s, a);
+    else hipLaunchKernelGGL((k_row<DT, TV, false, FAST>), grid, dim3(RT), 0, s, a);
+}
+template <int DT, bool FAST>
+void launch_row(const KArgs& a, hipStream_t s) {
+    static const int tv = env_int("AXS_ROW_TV", 4);
+    if (tv == 4) launch_row_tv<DT, FAST, 4>(a, s);
+    else launch_row_tv<DT, FAST, 8>(a, s);
+}
+
 // fast: 16-byte aligned rows of whole vectors (every segment end, a multiple
 // of MIN_CHUNK or the vocabulary, is then a multiple of the vector width)
 template <int DT>
 void launch_stream_dt(const Plan& pl, const KArgs& a, hipStream_t s) {
     const bool fast = a.vec && a.vocab % (DT == AXS_DTYPE_BF16 ? 8 : 4) == 0;
     if (pl.wide) {
-        if (fast) launch_stream_tv<DT, 1024, ROW_MAX, true>(a, s);
-        else launch_stream_tv<DT, 1024, ROW_MAX, false>(a, s);
+        if (fast) launch_row<DT, true>(a, s);
+        else launch_row<DT, false>(a, s);
     } else {
         if (fast) launch_stream_tv<DT, NT_CHUNK, SEG_MAX, true>(a, s);
         else launch_stream_tv<DT, NT_CHUNK, SEG_MAX, false>(a, s);

@@ -140,7 +140,10 @@ typedef struct axs_outputs {
                               (crates/ax-engine-mlx/src/sampling.rs:156-160)      */
     uint32_t* flags;       /* [batch] or NULL, AXS_FLAG_* bits                    */
     uint32_t* kept_ids;    /* [batch, kept_cap] or NULL: the kept set in draw order
-                              (diagnostics, e.g. top-k set parity)                */
+                              (diagnostics, e.g. top-k set parity).  Rows of the
+                              exact path list kept entries whose probability is
+                              below 2^-24 of the maximum's (never drawn) as
+                              0xFFFFFFFF after the ordered prefix                 */
     uint32_t* kept_count;  /* [batch] or NULL: size of the kept set               */
     int32_t   kept_cap;
     int32_t   reserved0;
