@@ -1,0 +1,175 @@
+"""GPU parity of the MTP speculative verify step (axs_mtp_verify, kernel
+k_mtp_verify over the pipeline's kept lists) against the CPU oracle's
+function-level law (crates/ax-engine-mlx/src/runner/mod.rs:12333-12462,
+crates/ax-engine-mlx/src/sampling.rs:647-752).
+
+Per sequence the emitted ids (accepted prefix + residual / bonus tail), their
+count and the accept count must equal the oracle's, except on sequences the
+oracle flags as near a decision boundary (|u - p/q| < 1e-6, or a near flag in
+one of the sequence's distributions), which are counted.  Draft ids are drawn
+from the draft law by the oracle with its own uniforms (config C5).
+"""
+import numpy as np
+import pytest
+
+from ax_sampler import _abi
+from ax_sampler.synth import DTYPE_BF16, DTYPE_F32, f32_to_bf16_bits, make_c5
+
+from gpu_common import log
+
+pytestmark = pytest.mark.gpu
+
+NEAR = _abi.MTP_FLAG_NEAR_ACCEPT | _abi.MTP_FLAG_NEAR
+
+
+@pytest.fixture(scope="module")
+def sampler():
+    from ax_sampler import HipSampler
+
+    s = HipSampler(0, max_batch=256, max_vocab=262144)
+    yield s
+    s.close()
+
+
+def _draft_ids(oracle, draft, dtype, B, D, V, dparams, seed):
+    """One token per draft row from the draft law (sample_categorical_into)."""
+    rows = draft.reshape(B * D, V)
+    p = np.repeat(dparams, D)
+    us = np.random.default_rng(seed).random(B * D).astype(np.float32)
+    ids, _, _ = oracle.sample_batch(rows, dtype, B * D, V, V, p, uniforms=us, nthreads=8,
+                                    explain=False)
+    return ids.reshape(B, D).astype(np.uint32)
+
+
+def _to_dev(a, dtype):
+    import torch
+
+    if dtype == DTYPE_BF16:
+        return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16).cuda()
+    return torch.from_numpy(np.ascontiguousarray(a)).cuda()
+
+
+def _run(sampler, oracle, tgt, dft, dtype, tp, dp, dids, us, name):
+    import torch
+
+    B, D1, V = tgt.shape
+    D = D1 - 1
+    res = sampler.mtp_verify(_to_dev(tgt, dtype), _to_dev(dft, dtype), dids, tp, dp, uniforms=us)
+    torch.cuda.synchronize()
+    g_ids = res.out_ids.cpu().numpy().view(np.uint32)
+    g_n = res.out_count.cpu().numpy().view(np.uint32)
+    g_ac = res.accept_count.cpu().numpy().view(np.uint32)
+    g_fl = res.flags.cpu().numpy().view(np.uint32)
+    c_ids, c_n, c_ac, c_fl = oracle.mtp_verify_batch(tgt, dft, dtype, B, D, V, V, dids, tp, dp,
+                                                     uniforms=us, nthreads=8)
+    near = (c_fl & np.uint32(NEAR)) != 0
+    bad = []
+    for b in range(B):
+        same = g_n[b] == c_n[b] and g_ac[b] == c_ac[b] and np.array_equal(g_ids[b, :g_n[b]],
+                                                                           c_ids[b, :c_n[b]])
+        if not same and not near[b]:
+            bad.append(b)
+    assert not bad, (f"{name}: sequences {bad[:8]} differ: gpu n={g_n[bad[:8]]} ac={g_ac[bad[:8]]} "
+                     f"ids={g_ids[bad[:8]].tolist()} | cpu n={c_n[bad[:8]]} ac={c_ac[bad[:8]]} "
+                     f"ids={c_ids[bad[:8]].tolist()} flags gpu={g_fl[bad[:8]]} cpu={c_fl[bad[:8]]}")
+    assert not np.any(g_fl & np.uint32(_abi.MTP_FLAG_ERROR)), f"{name}: error flag"
+    tail = (g_fl & np.uint32(_abi.MTP_FLAG_RESIDUAL | _abi.MTP_FLAG_BONUS)) != 0
+    summ = {"seqs": B, "near": int(near.sum()), "accepted": int(g_ac.sum()),
+            "residual": int(np.count_nonzero(g_fl & np.uint32(_abi.MTP_FLAG_RESIDUAL))),
+            "bonus": int(np.count_nonzero(g_fl & np.uint32(_abi.MTP_FLAG_BONUS))), "tail": int(tail.sum())}
+    log(f"{name}: {summ}")
+    return summ, g_ac
+
+
+def test_c5_full(sampler, oracle):
+    t, d, tp, dp = make_c5(5)
+    B, D1, V = t.shape
+    D = D1 - 1
+    dids = _draft_ids(oracle, d, DTYPE_BF16, B, D, V, dp, 55)
+    us = np.random.default_rng(505).random((B, D + 1)).astype(np.float32)
+    s, _ = _run(sampler, oracle, t, d, DTYPE_BF16, tp, dp, dids, us, "C5")
+    assert s["accepted"] > 0 and s["residual"] + s["bonus"] == B
+
+
+def test_c5_philox(sampler, oracle):
+    t, d, tp, dp = make_c5(15)
+    B, D1, V = t.shape
+    dids = _draft_ids(oracle, d, DTYPE_BF16, B, D1 - 1, V, dp, 56)
+    _run(sampler, oracle, t, d, DTYPE_BF16, tp, dp, dids, None, "C5-philox")
+
+
+def test_accept_all_and_reject_first(sampler, oracle):
+    t, d, tp, dp = make_c5(25, B=16, V=32768)
+    B, D1, V = t.shape
+    D = D1 - 1
+    dids = _draft_ids(oracle, d, DTYPE_BF16, B, D, V, dp, 57)
+    us = np.zeros((B, D + 1), np.float32)
+    us[:, D] = np.linspace(0.02, 0.98, B)
+    s, ac = _run(sampler, oracle, t, d, DTYPE_BF16, tp, dp, dids, us, "accept-all")
+    assert s["bonus"] == B and np.all(ac == D)
+    us[:, :D] = 1.0  # u < min(1, p/q) never holds for u = 1: every first draft rejected
+    s, ac = _run(sampler, oracle, t, d, DTYPE_BF16, tp, dp, dids, us, "reject-first")
+    assert np.all(ac == 0) and s["residual"] == B
+
+
+def test_draft_equals_target(sampler, oracle):
+    """q == p: the residual max(p - q, 0) is empty and falls back to the target."""
+    t, _, tp, dp = make_c5(35, B=8, V=16384)
+    B, D1, V = t.shape
+    D = D1 - 1
+    d = np.ascontiguousarray(t[:, :D, :])
+    dp = tp.copy()
+    dids = _draft_ids(oracle, d, DTYPE_BF16, B, D, V, dp, 58)
+    us = np.random.default_rng(508).random((B, D + 1)).astype(np.float32)
+    us[: B // 2, 0] = 1.0
+    _run(sampler, oracle, t, d, DTYPE_BF16, tp, dp, dids, us, "draft==target")
+
+
+@pytest.mark.parametrize("dtype,B,D,V", [(DTYPE_F32, 24, 1, 4099), (DTYPE_BF16, 8, 7, 8192),
+                                         (DTYPE_F32, 12, 2, 50000)])
+def test_depths_and_dtypes(sampler, oracle, dtype, B, D, V):
+    rng = np.random.default_rng([B, D, V])
+    t = (rng.standard_normal((B, D + 1, V), dtype=np.float32) * np.float32(3.0))
+    d = t[:, :D, :] + rng.standard_normal((B, D, V), dtype=np.float32) * np.float32(0.5)
+    if dtype == DTYPE_BF16:
+        t, d = f32_to_bf16_bits(t), f32_to_bf16_bits(d)
+    _, _, tp, dp = make_c5(45, B=B, depth=D, V=16)
+    tp["temperature"] = rng.choice(np.array([0.6, 1.0, 1.4], np.float32), B)
+    tp["top_k"] = rng.choice(np.array([20, 40], np.uint32), B)
+    dp["temperature"] = tp["temperature"] * np.float32(0.9)
+    dp["top_k"] = tp["top_k"]
+    dids = _draft_ids(oracle, d, dtype, B, D, V, dp, 59)
+    us = rng.random((B, D + 1)).astype(np.float32)
+    _run(sampler, oracle, t, d, dtype, tp, dp, dids, us, f"mtp dtype={dtype} B={B} D={D} V={V}")
+
+
+def test_kept_set_beyond_capacity_declines(sampler, oracle):
+    """A distribution keeping more than 2,048 ids (the device kept-list
+    capacity) is declined: error flag, no ids (the caller falls back to the
+    CPU law); sequences within capacity are unaffected."""
+    import torch
+
+    rng = np.random.default_rng(77)
+    B, D, V = 4, 1, 8192
+    t = rng.standard_normal((B, D + 1, V), dtype=np.float32) * np.float32(0.3)
+    d = t[:, :D, :] + rng.standard_normal((B, D, V), dtype=np.float32) * np.float32(0.05)
+    _, _, tp, dp = make_c5(46, B=B, depth=D, V=16)
+    tp["temperature"] = 1.0
+    tp["top_p"] = 0.95
+    tp["top_k"] = np.array([0, 40, 0, 40], np.uint32)  # rows 0, 2: ~7,000 ids kept
+    dp["temperature"] = 1.0
+    dp["top_k"] = 40
+    dids = _draft_ids(oracle, d, DTYPE_F32, B, D, V, dp, 60)
+    us = rng.random((B, D + 1)).astype(np.float32)
+    res = sampler.mtp_verify(_to_dev(t, DTYPE_F32), _to_dev(d, DTYPE_F32), dids, tp, dp, uniforms=us)
+    torch.cuda.synchronize()
+    fl = res.flags.cpu().numpy().view(np.uint32)
+    n = res.out_count.cpu().numpy().view(np.uint32)
+    err = (fl & np.uint32(_abi.MTP_FLAG_ERROR)) != 0
+    assert list(err) == [True, False, True, False], fl
+    assert n[0] == 0 and n[2] == 0 and n[1] >= 1 and n[3] >= 1
+    c_ids, c_n, c_ac, _ = oracle.mtp_verify_batch(t, d, DTYPE_F32, B, D, V, V, dids, tp, dp,
+                                                  uniforms=us, nthreads=4)
+    g_ids = res.out_ids.cpu().numpy().view(np.uint32)
+    for b in (1, 3):
+        assert n[b] == c_n[b] and np.array_equal(g_ids[b, :n[b]], c_ids[b, :c_n[b]])
