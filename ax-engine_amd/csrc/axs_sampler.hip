@@ -123,6 +123,11 @@ __device__ __forceinline__ ChunkStat sub_stat(const ChunkStat* p) {
 // waits until every memory operation this thread issued has completed
 __device__ __forceinline__ void wait_mem() { __builtin_amdgcn_s_waitcnt(0); }
 
+// Workgroup barrier for data exchanged through LDS only: waits for this
+// wave's LDS (and scalar) operations, not for its outstanding global loads,
+// which stay in flight across it (__syncthreads would drain them).
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 struct RowState {
     float m;
     float inv;
@@ -375,15 +380,16 @@ __device__ __forceinline__ void hist_each(const KArgs& a, const RowCtx& c, const
 // f(t) for every token t in [lo, hi) that the no-repeat n-gram rule bans
 // (logits_with_no_repeat_ngram_in_place, sampling.rs:896-920), spread over
 // the block
-template <int NT, typename F>
-__device__ __forceinline__ void ngram_each(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi, F&& f) {
+template <typename F>
+__device__ __forceinline__ void ngram_each_g(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi, int64_t first,
+                                             int64_t stride, F&& f) {
     const int64_t nhist = c.w1 - c.h0;
     const uint32_t ng = c.p.no_repeat_ngram_size;
     int64_t keep = (int64_t)(c.p.ngram_window > ng ? c.p.ngram_window : ng);
     if (keep > nhist) keep = nhist;
     const int64_t hs = c.w1 - keep;
     const int64_t plen = (int64_t)ng - 1;
-    for (int64_t s = threadIdx.x; s + (int64_t)ng <= keep; s += NT) {
+    for (int64_t s = first; s + (int64_t)ng <= keep; s += stride) {
         bool match = true;
         for (int64_t j = 0; j < plen; ++j)
             if (a.hist[hs + s + j] != a.hist[c.w1 - plen + j]) {
@@ -395,6 +401,10 @@ __device__ __forceinline__ void ngram_each(const KArgs& a, const RowCtx& c, uint
             if (t >= lo && t < hi) f(t);
         }
     }
+}
+template <int NT, typename F>
+__device__ __forceinline__ void ngram_each(const KArgs& a, const RowCtx& c, uint32_t lo, uint32_t hi, F&& f) {
+    ngram_each_g(a, c, lo, hi, (int64_t)threadIdx.x, (int64_t)NT, f);
 }
 
 // Marks the segment's special ids (ids in [lo, hi)) and lists its bias
@@ -788,19 +798,32 @@ struct FinLds {
     uint32_t n;
 };
 
-// Decisions over n sorted candidates (F.key), run by wave 0.  The reference
-// walks the candidates with f32 running sums (sampling.rs:283-316, 922-952):
-// the top-p total, the nucleus cut, the filtered sum and the draw all read
-// the same running sums S[i] = fl(S[i-1] + p_i) in the same order, so one
-// sequential pass computes them (lane 0) and the cuts are binary searches.
+// first index i in [lo, hi) with S[i] >= t for non-decreasing S (hi if
+// none), by the whole wave: one read per lane when the range fits in a wave,
+// else a binary search (every lane the same, so the reads are broadcasts)
+__device__ __forceinline__ uint32_t first_ge_wave(const float* S, uint32_t lo, uint32_t hi, float t) {
+    const int lane = threadIdx.x & 63;
+    if (hi - lo <= 64u) {
+        const uint32_t i = lo + (uint32_t)lane;
+        const uint64_t m = __ballot(i < hi && S[i] >= t);
+        return m ? lo + (uint32_t)__builtin_ctzll(m) : hi;
+    }
+    return first_ge(S, lo, hi, t);
+}
+
+// Decisions over n sorted candidates (F.key), run by one wave with the
+// row's uniform u.  The reference walks the candidates with f32 running sums
+// (sampling.rs:283-316, 922-952): the top-p total, the nucleus cut, the
+// filtered sum and the draw all read the same running sums
+// S[i] = fl(S[i-1] + p_i) in the same order, so one sequential pass computes
+// them (lane 0) and the cuts are searches.
 template <int NT>
 __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_sampling_params& p, uint32_t mode,
-                                              bool sorted, FinLds<NT>& F, uint32_t n, uint32_t flags0) {
+                                              bool sorted, FinLds<NT>& F, uint32_t n, uint32_t flags0, float u) {
     const int lane = threadIdx.x & 63;
     auto P = [&](uint64_t k) { return sorted ? pdesc_p(k) : idasc_p(k); };
     auto ID = [&](uint64_t k) { return sorted ? pdesc_id(k) : idasc_id(k); };
     const uint32_t L = n;
-    uint32_t kept = 0;
     if (lane == 0) {
         float acc = 0.0f;
         uint32_t i = 0;
@@ -818,46 +841,49 @@ __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_s
             acc = __fadd_rn(acc, P(F.key[i]));
             F.S[i] = acc;
         }
-        const float* S = F.S;
-        uint32_t flags = flags0 | AXS_FLAG_DREW;
-        uint32_t nk = L;
-        if (sorted && topp_active(p)) {
-            // top-p over the full candidate mass (sampling.rs:931-945)
-            const float total = S[L - 1];
-            const float cutoff = __fmul_rn(p.top_p, total);
-            const uint32_t j = first_ge(S, 0, L, cutoff);
-            nk = j < L ? j + 1 : L;
-            const double up = (double)S[nk - 1] - (double)cutoff;
-            const double lo = nk >= 2 ? (double)cutoff - (double)S[nk - 2] : INFINITY;
-            if (fmin(up, lo) / (double)total < 1e-6 && (p.top_k == 0 || nk <= p.top_k))
-                flags |= AXS_FLAG_NEAR_NUCLEUS;
-        }
-        kept = nk;
-        if (sorted && p.top_k > 0 && kept > p.top_k) kept = p.top_k;
-        if (sorted && kept < L) {
-            const float pa = P(F.key[kept - 1]);
-            const float pb = P(F.key[kept]);
-            // near but not identical probabilities across the cut (identical
-            // ones come from equal logits and are ordered by id everywhere)
-            if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
-        }
-        const float Fs = S[kept - 1];
-        const float u = row_uniform(a, r, p);
-        const float thr = __fmul_rn(u, Fs);
-        uint32_t j = first_ge(S, 0, kept, thr);
-        if (j == kept) {
-            // last maximum (sampling.rs:310-315); unreachable for u <= 1
-            float bp = -1.0f;
-            for (uint32_t i2 = 0; i2 < kept; ++i2)
-                if (P(F.key[i2]) >= bp) {
-                    bp = P(F.key[i2]);
-                    j = i2;
-                }
-        } else {
-            const double up = (double)S[j] - (double)thr;
-            const double lo = j > 0 ? (double)thr - (double)S[j - 1] : INFINITY;
-            if (fmin(up, lo) / (double)Fs < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
-        }
+    }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    const float* S = F.S;
+    uint32_t flags = flags0 | AXS_FLAG_DREW;
+    uint32_t nk = L;
+    if (sorted && topp_active(p)) {
+        // top-p over the full candidate mass (sampling.rs:931-945)
+        const float total = S[L - 1];
+        const float cutoff = __fmul_rn(p.top_p, total);
+        const uint32_t j = first_ge_wave(S, 0, L, cutoff);
+        nk = j < L ? j + 1 : L;
+        const double up = (double)S[nk - 1] - (double)cutoff;
+        const double lo = nk >= 2 ? (double)cutoff - (double)S[nk - 2] : INFINITY;
+        if (fmin(up, lo) / (double)total < 1e-6 && (p.top_k == 0 || nk <= p.top_k)) flags |= AXS_FLAG_NEAR_NUCLEUS;
+    }
+    uint32_t kept = nk;
+    if (sorted && p.top_k > 0 && kept > p.top_k) kept = p.top_k;
+    if (sorted && kept < L) {
+        const float pa = P(F.key[kept - 1]);
+        const float pb = P(F.key[kept]);
+        // near but not identical probabilities across the cut (identical
+        // ones come from equal logits and are ordered by id everywhere)
+        if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
+    }
+    const float Fs = S[kept - 1];
+    const float thr = __fmul_rn(u, Fs);
+    uint32_t j = first_ge_wave(S, 0, kept, thr);
+    if (j == kept) {
+        // last maximum (sampling.rs:310-315); unreachable for u <= 1
+        float bp = -1.0f;
+        for (uint32_t i2 = 0; i2 < kept; ++i2)
+            if (P(F.key[i2]) >= bp) {
+                bp = P(F.key[i2]);
+                j = i2;
+            }
+    } else {
+        const double up = (double)S[j] - (double)thr;
+        const double lo = j > 0 ? (double)thr - (double)S[j - 1] : INFINITY;
+        if (fmin(up, lo) / (double)Fs < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
+    }
+    if (lane == 0) {
         const float pj = P(F.key[j]);
         write_row(a, r, ID(F.key[j]), logprob_of(__fdiv_rn(pj, Fs)), flags);
         if (a.out_kept_count) a.out_kept_count[r] = kept;
@@ -868,7 +894,6 @@ __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_s
             a.rstate[r].flags = flags;
         }
     }
-    kept = (uint32_t)__builtin_amdgcn_readlane((int)kept, 0);
     if (a.out_kept && a.out_kept_cap > 0) {
         const uint32_t nw = kept < (uint32_t)a.out_kept_cap ? kept : (uint32_t)a.out_kept_cap;
         for (uint32_t i = lane; i < nw; i += 64) a.out_kept[(size_t)r * a.out_kept_cap + i] = ID(F.key[i]);
@@ -1004,7 +1029,7 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
                 block_sort_desc<NT>(F.key, np2);
             }
             __syncthreads();
-            if (tid < 64) decide_sorted<NT>(a, r, p, mode, sorted, F, n, flags0);
+            if (tid < 64) decide_sorted<NT>(a, r, p, mode, sorted, F, n, flags0, row_uniform(a, r, p));
         }
     }
     if (exact && tid == 0) list_exact(a, r, p, m, inv, mode, sorted, am);
@@ -1013,40 +1038,70 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
 // A min-p row decided by one wave from n <= 256 gathered candidates (a
 // superset of its min-p survivors, sampling.rs:283-294): survivors p =
 // exp((l - m) / T) >= min_p, ordered by (p desc, id asc) — or by id for an
-// index-order draw — with a bitonic sort in registers, then decide_sorted.
-// Called by the 64 lanes of one wave; no block barriers.
-template <int NT>
+// index-order draw — then decide_sorted.  A candidate whose (l - m) / T is
+// more than 1e-5 from ln(min_p) is classified without its exact exp (rounding
+// moves exp by < 2^-24 relative); survivors get the correctly rounded one.
+// The survivors' keys are compacted by ballot into kbuf (LDS scratch of 256
+// keys, free once the candidates are read), then ranked (at most 64) or
+// bitonic-sorted.  cand_at(k) is the k-th candidate; lnmin = ln(min_p) and u
+// the row's uniform.  Called by the 64 lanes of one wave; no block barriers.
+template <int NT, typename CA>
 __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
-                                 uint32_t am, uint32_t n, const Cand* cand, FinLds<NT>& F) {
+                                                 uint32_t am, uint32_t n, CA&& cand_at, uint64_t* kbuf,
+                                                 FinLds<NT>& F, double lnmin, float u) {
     const int lane = threadIdx.x & 63;
     const bool sorted = filters_enabled(p);
-    uint64_t k[4];
-    float mg = INFINITY;
-    uint32_t ns = 0;
+    Cand mine[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const uint32_t i = (uint32_t)lane + 64u * (uint32_t)j;
-        k[j] = 0ull;
-        bool keep = false;
-        if (i < n) {
-            const Cand cd = cand[i];
-            const float pr = prob_of(cd.l, m, inv);
-            mg = fminf(mg, fabsf(pr - p.min_p) / p.min_p);
-            keep = pr >= p.min_p;
-            if (keep) k[j] = sorted ? key_pdesc(pr, cd.id) : key_idasc(pr, cd.id);
-        }
-        ns += (uint32_t)__popcll(__ballot(keep));
+        mine[j] = i < n ? cand_at(i) : Cand{NONE, -INFINITY};
     }
-    mg = -wave_max_dpp(-mg);
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    bool near = false;
+    uint32_t ns = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        bool keep = false;
+        uint64_t key = 0;
+        if (mine[j].id != NONE) {
+            const float x = __fmul_rn(__fsub_rn(mine[j].l, m), inv);
+            const double dx = (double)x - lnmin;
+            float pr = 0.0f;
+            if (dx >= -1e-5) {
+                pr = prob_of(mine[j].l, m, inv);
+                keep = pr >= p.min_p;
+                if (dx <= 1e-5) near |= fabsf(pr - p.min_p) / p.min_p < 1e-6f;
+            }
+            if (keep) key = sorted ? key_pdesc(pr, mine[j].id) : key_idasc(pr, mine[j].id);
+        }
+        const uint64_t bk = __ballot(keep);
+        if (keep) kbuf[ns + mbcnt64(bk)] = key;
+        ns += (uint32_t)__popcll(bk);
+    }
+    const bool anynear = __ballot(near) != 0ull;
     if (ns == 0) {  // (unreachable: the maximum itself has p = 1)
         if (lane == 0) list_exact(a, r, p, m, inv, M_MINP, sorted, am);
         return;
     }
-    // survivors' keys are > 0, the empty slots 0: survivors come first
-    if (n <= 64) {
-        k[0] = wave_sort_desc(k[0]);
-        if ((uint32_t)lane < ns) F.key[lane] = k[0];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // keys are distinct; survivors' keys are > 0
+    if (ns <= 64) {
+        const uint64_t my = (uint32_t)lane < ns ? kbuf[lane] : 0ull;
+        uint32_t rank = 0;
+        for (uint32_t j = 0; j < ns; ++j) rank += kbuf[j] > my ? 1u : 0u;
+        if ((uint32_t)lane < ns) F.key[rank] = my;
     } else {
+        uint64_t k[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t i = (uint32_t)lane + 64u * (uint32_t)j;
+            k[j] = i < ns ? kbuf[i] : 0ull;
+        }
         wave_sort_desc4(k);
 #pragma unroll
         for (int j = 0; j < 4; ++j)
@@ -1055,7 +1110,7 @@ __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const ax
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    decide_sorted<NT>(a, r, p, M_MINP, sorted, F, ns, mg < 1e-6f ? AXS_FLAG_NEAR_MINP : 0u);
+    decide_sorted<NT>(a, r, p, M_MINP, sorted, F, ns, anynear ? AXS_FLAG_NEAR_MINP : 0u, u);
 }
 
 // Merges the published results of the nseg segments of row r and decides it.
@@ -1603,7 +1658,8 @@ constexpr int HWAVES = 2;              // waves that fetch the window before the
 constexpr uint32_t HPRE = 2048;        // window tokens staged through LDS
 constexpr uint32_t HBITS = 12;
 constexpr uint32_t HSZ = 1u << HBITS;  // hash slots
-constexpr uint32_t CAPW = 384;         // captured special elements per wave
+constexpr uint32_t CAPW = 256;         // captured special elements per wave
+constexpr uint32_t CANDW = 256;        // min-p candidates per wave
 constexpr uint32_t RBCAP = 1024;       // bias entries per row
 constexpr uint32_t HV_CNT = 0x000FFFFFu;  // window count
 constexpr uint32_t HV_BSH = 20;           // bias entry index + 1, or HV_BMULTI
@@ -1623,10 +1679,9 @@ struct RowLds {
         } p;
         FinLds<RT> F;
     } u;
-    union {
-        uint32_t stage[HPRE];
-        Cand cand[FIN_CAP];
-    } v;
+    Cand cand[RWV][CANDW];  // each wave's min-p candidates (ballot slots)
+    uint32_t wcn[RWV];      // their counts
+    uint32_t stage[HPRE];  // the window's first tokens (read by the hash build during the stream)
     Cand cap[RWV][CAPW];
     uint32_t bias_id[RBCAP];
     float bias_v[RBCAP];
@@ -1635,7 +1690,7 @@ struct RowLds {
     uint32_t wa[RWV];   // ... and its lowest id
     float gm[RWV];      // per-wave greedy logprob partials: maximum ...
     float gs[RWV];      // ... and sum of exp(l - maximum)
-    uint32_t ncand, next, nbias, err;
+    uint32_t next, nbias, err;
     uint32_t bpos;  // some bias entry is not <= 0 (it may raise a logit)
     int gmax;       // shared lower bound of the row maximum (ordered-int encoding)
 };
@@ -1774,7 +1829,6 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     }
     if (tid == 0) {
         SL.next = 2u * NW;
-        SL.ncand = 0;
         SL.err = 0;
         SL.bpos = 0;
         SL.gmax = f2ord(-INFINITY);
@@ -1816,20 +1870,41 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         }
         if (wv < HWAVES) {
 #pragma unroll
-            for (int k = 0; k < HK; ++k) SL.v.stage[tid + k * (HWAVES * 64)] = ht[k];
+            for (int k = 0; k < HK; ++k) SL.stage[tid + k * (HWAVES * 64)] = ht[k];
         }
     }
-    __syncthreads();
+    lds_barrier();
+    // The bitmap, which the stream needs, is marked by every thread; the hash
+    // (window counts, bias entries, bans), which only the specials' pass
+    // after the stream needs, is built by the window waves while the others
+    // already stream.
+    uint32_t* spec = SL.u.p.spec;
+    uint32_t* hkey = SL.u.p.hkey;
+    uint32_t* hval = SL.u.p.hval;
     if (special) {
-        uint32_t* spec = SL.u.p.spec;
-        uint32_t* hkey = SL.u.p.hkey;
-        uint32_t* hval = SL.u.p.hval;
-        auto mark = [&](uint32_t t) { atomicOr(&spec[t >> 5], 1u << (t & 31u)); };
+        auto mark = [&](uint32_t t) {
+            if (t < hi) atomicOr(&spec[t >> 5], 1u << (t & 31u));  // ids outside the vocabulary are skipped
+        };
+        if (c.cnt_on) {
+#pragma unroll
+            for (int k = 0; k < (int)(HPRE / RT); ++k) {
+                const uint32_t t = SL.stage[tid + k * RT];
+                if (t != NONE) mark(t);
+            }
+            for (int64_t i = c.w0 + HPRE + tid; i < c.w1; i += RT) mark(a.hist[i]);
+        }
+        if (c.bias_on) {
+            if (c.b1 - c.b0 > (int64_t)RBCAP && tid == 0) SL.err |= RERR_BIAS;
+            for (uint32_t j = tid; j < SL.nbias; j += RT) mark(SL.bias_id[j]);
+        }
+        if (c.ban_on) ngram_each<RT>(a, c, lo, hi, mark);
+        lds_barrier();
+    }
+    auto build_hash = [&]() {  // waves 0..HWAVES-1
+        constexpr int HL = HWAVES * 64;
         bool full = false;
         auto count = [&](uint32_t t) {
-            if (t >= hi) return;  // ids outside the vocabulary are skipped
-            mark(t);              // (the bitmap is always complete)
-            if (full) return;
+            if (t >= hi || full) return;
             const uint32_t s = hash_insert(hkey, t);
             if (s == NONE) full = true;
             else atomicAdd(&hval[s], 1u);
@@ -1837,20 +1912,16 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         if (c.cnt_on) {
             if (c.w1 - c.w0 > (int64_t)HV_CNT) full = true;  // counts would not fit
 #pragma unroll
-            for (int k = 0; k < (int)(HPRE / RT); ++k) {
-                const uint32_t t = SL.v.stage[tid + k * RT];
+            for (int k = 0; k < (int)(HPRE / HL); ++k) {
+                const uint32_t t = SL.stage[tid + k * HL];
                 if (t != NONE) count(t);
             }
-            for (int64_t i = c.w0 + HPRE + tid; i < c.w1; i += RT) count(a.hist[i]);
+            for (int64_t i = c.w0 + HPRE + tid; i < c.w1; i += HL) count(a.hist[i]);
         }
         if (c.bias_on) {
-            if (c.b1 - c.b0 > (int64_t)RBCAP) {
-                if (tid == 0) SL.err |= RERR_BIAS;
-            }
-            for (uint32_t j = tid; j < SL.nbias; j += RT) {
+            for (uint32_t j = tid; j < SL.nbias; j += HL) {
                 const uint32_t t = SL.bias_id[j];
                 if (t >= hi) continue;
-                mark(t);
                 const uint32_t s = hash_insert(hkey, t);
                 if (s == NONE) {
                     full = true;
@@ -1868,16 +1939,13 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             }
         }
         if (c.ban_on)
-            ngram_each<RT>(a, c, lo, hi, [&](uint32_t t) {
-                mark(t);
+            ngram_each_g(a, c, lo, hi, (int64_t)tid, (int64_t)HL, [&](uint32_t t) {
                 const uint32_t s = hash_insert(hkey, t);
                 if (s == NONE) full = true;
                 else atomicOr(&hval[s], HV_BAN);
             });
         if (full) atomicOr(&SL.err, RERR_HASH);
-        __syncthreads();
-    }
-    const bool hfull = special && (SL.err & RERR_HASH);
+    };
 
     const uint32_t mode = c.mode;
     const float inv = __fdiv_rn(1.0f, c.p.temperature);
@@ -1920,12 +1988,18 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         }
         rthr = !fastp ? -INFINITY : (gather ? fminf(lpre, mrun) : mrun);
     };
-    auto add_cand = [&](uint32_t e, float l) {
-        const uint32_t slot = atomicAdd(&SL.ncand, 1u);
-        if (slot < FIN_CAP) {
-            SL.v.cand[slot].id = e;
-            SL.v.cand[slot].l = l;
+    // The wave's min-p candidates: slots by ballot (every lane of the wave
+    // calls these; wcand is the wave's running count)
+    Cand* candw = SL.cand[wv];
+    uint32_t wcand = 0;
+    auto append_one = [&](bool c, uint32_t e, float l) {
+        const uint64_t m1 = __ballot(c);
+        const uint32_t pos = wcand + mbcnt64(m1);
+        if (c && pos < CANDW) {
+            candw[pos].id = e;
+            candw[pos].l = l;
         }
+        wcand += (uint32_t)__popcll(m1);
     };
     auto gsum_add = [&](float l) {
         if (isfinite(l)) {
@@ -2026,7 +2100,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     // read as NaN, disallowed ones -inf; the lane's maximum, min-p candidates
     // and the greedy logprob sum updated.  Runs with only the relevant lanes
     // active (the capture, whose ballots need the whole wave, is done before).
-    auto look = [&](const u32x4& raw, uint32_t mw, uint32_t e0, uint32_t sk) __attribute__((always_inline)) {
+    auto look = [&](const u32x4& raw, uint32_t mw, uint32_t e0, uint32_t sk) __attribute__((always_inline)) -> uint32_t {
         float v[EPV];
         vec_vals(raw, mw, e0, sk, v);
         float vm = v[0];
@@ -2038,28 +2112,52 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             traw = raw;
             tmw = mw;
         }
+        uint32_t qm = 0;  // the vector's min-p candidates
         if (gather && vm >= lpre) {
-            // one slot reservation for all of the vector's candidates
-            uint32_t qm = 0;
 #pragma unroll
             for (int q = 0; q < EPV; ++q)
                 if (v[q] >= lpre && __fmul_rn(__fsub_rn(v[q], mrun), inv) >= thr) qm |= 1u << q;
-            if (qm) {
-                uint32_t slot = atomicAdd(&SL.ncand, (uint32_t)__popc(qm));
-#pragma unroll
-                for (int q = 0; q < EPV; ++q)
-                    if ((qm >> q) & 1u) {
-                        if (slot < FIN_CAP) {
-                            SL.v.cand[slot].id = e0 + q;
-                            SL.v.cand[slot].l = v[q];
-                        }
-                        ++slot;
-                    }
-            }
         }
         if (gsum_on) {
 #pragma unroll
             for (int q = 0; q < EPV; ++q) gsum_add(v[q]);
+        }
+        return qm;
+    };
+    // Appends the vector's candidates (bits qm; a candidate is neither special
+    // nor disallowed, so its value is the raw element).  Whole wave.
+    auto append = [&](const u32x4& raw, uint32_t e0, uint32_t qm) {
+        const uint64_t m1 = __ballot(qm != 0u);
+        if (m1 == 0ull) return;
+        const uint64_t m2 = __ballot((qm & (qm - 1u)) != 0u);
+        if (m2 == 0ull) {
+            const uint32_t pos = wcand + mbcnt64(m1);
+            if (qm != 0u && pos < CANDW) {
+                const uint32_t q = (uint32_t)__ffs((int)qm) - 1u;
+                candw[pos].id = e0 + q;
+                candw[pos].l = elem(raw, q);
+            }
+            wcand += (uint32_t)__popcll(m1);
+        } else {
+            const uint32_t c = (uint32_t)__popc(qm);
+            uint32_t pre = 0, tot = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const uint64_t mb = __ballot((c >> b) & 1u);
+                pre += mbcnt64(mb) << b;
+                tot += (uint32_t)__popcll(mb) << b;
+            }
+            uint32_t pos = wcand + pre;
+#pragma unroll
+            for (int q = 0; q < EPV; ++q)
+                if ((qm >> q) & 1u) {
+                    if (pos < CANDW) {
+                        candw[pos].id = e0 + q;
+                        candw[pos].l = unpack<DT>(raw, q);
+                    }
+                    ++pos;
+                }
+            wcand += tot;
         }
     };
     // Per vector: its raw maximum (special and disallowed elements included)
@@ -2081,7 +2179,9 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                 // whole wave: the capture keeps a wave-uniform count
                 const uint32_t sk = rel ? spec_bits(e0) : 0u;
                 if (special) capture(T.raw[j], mw, e0, sk);
-                if (rel) look(T.raw[j], mw, e0, sk);
+                uint32_t qm = 0;
+                if (rel) qm = look(T.raw[j], mw, e0, sk);
+                if (gather) append(T.raw[j], e0, qm);
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -2122,6 +2222,25 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         load(T, ch);
         if (bound) raise(wave_max_dpp(tm));
     };
+    if (false) {
+        // every wave's first chunk seeds the bound with the block maximum
+        const float tmx = wave_max_dpp(c0 < nchunk ? tile_max(b0, c0) : -INFINITY);
+        if (lane == 0) SL.wm[wv] = tmx;
+        lds_barrier();
+        float mm = SL.wm[0];
+#pragma unroll
+        for (int k = 1; k < RWV; ++k) mm = fmaxf(mm, SL.wm[k]);
+        mrun = mm;
+        set_pre();
+    }
+    if (special && wv < HWAVES) build_hash();
+    // the decision's per-row constants, off its critical path
+    double lnmin = 0.0;
+    float urow = 0.0f;
+    if (gather && wv == 0) {
+        lnmin = log((double)c.p.min_p);
+        urow = row_uniform(a, r, c.p);
+    }
     // Both buffers are refilled unconditionally (a claim past the end loads a
     // dummy line), so the wait for one buffer leaves the other's loads in
     // flight.  Claims only grow: once one is past the end, so are all later.
@@ -2141,29 +2260,37 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         ta = tj + q0;
     }
     if (special && lane == 0 && wcnt > CAPW) atomicOr(&SL.err, RERR_CAP);
-    __syncthreads();
+    lds_barrier();
     // the special ids' processed values
     if (special) {
-        auto visit = [&](uint32_t e, float l) {
-            am_merge(tm, ta, l, isnan(l) ? NONE : e);
-            if (gather && l > -INFINITY && (mrun == -INFINITY || __fmul_rn(__fsub_rn(l, mrun), inv) >= thr))
-                add_cand(e, l);
-            if (gsum_on) gsum_add(l);
+        auto cand_ok = [&](float l) {
+            return gather && l > -INFINITY && (mrun == -INFINITY || __fmul_rn(__fsub_rn(l, mrun), inv) >= thr);
         };
         if (!(SL.err & (RERR_HASH | RERR_CAP))) {
-            // each wave its own captures
-            for (uint32_t i = (uint32_t)lane; i < wcnt; i += 64u) {
-                const Cand cd = capw[i];
-                const uint32_t e = cd.id & ~CAP_OFF;
-                const uint32_t s = hash_find(SL.u.p.hkey, e);
-                const uint32_t hv = s == NONE ? 0u : SL.u.p.hval[s];
-                visit(e, row_special_value(c, SL, e, cd.l, hv & HV_CNT, (hv >> HV_BSH) & HV_BMULTI,
-                                           (hv & HV_BAN) != 0u, (cd.id & CAP_OFF) != 0u));
+            // each wave its own captures (whole-wave loop: the appends ballot)
+            for (uint32_t base = 0; base < wcnt; base += 64u) {
+                const uint32_t i = base + (uint32_t)lane;
+                const bool ok = i < wcnt;
+                uint32_t e = 0;
+                float l = NAN;
+                if (ok) {
+                    const Cand cd = capw[i];
+                    e = cd.id & ~CAP_OFF;
+                    const uint32_t s = hash_find(SL.u.p.hkey, e);
+                    const uint32_t hv = s == NONE ? 0u : SL.u.p.hval[s];
+                    l = row_special_value(c, SL, e, cd.l, hv & HV_CNT, (hv >> HV_BSH) & HV_BMULTI,
+                                          (hv & HV_BAN) != 0u, (cd.id & CAP_OFF) != 0u);
+                    am_merge(tm, ta, l, isnan(l) ? NONE : e);
+                    if (gsum_on) gsum_add(l);
+                }
+                if (gather) append_one(ok && cand_ok(l), e, l);
             }
+            if (lane == 0) SL.wcn[wv] = wcand;
         } else {
             // a full hash or capture region: every special id resolved from
             // HBM (raw logit; window count and ban from the hash, or, when it
-            // is full, by scanning the history)
+            // is full, by scanning the history); candidates by LDS atomics
+            if (lane == 0) SL.wcn[wv] = wcand;
             const bool hok = !(SL.err & RERR_HASH);
             const uint32_t nw = (hi + 31u) / 32u;
             for (uint32_t wi = tid; wi < nw; wi += RT) {
@@ -2187,10 +2314,21 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                         ban = (cw & CNT_BAN) != 0u;
                     }
                     const bool off = c.mask_on && !((a.mask[(size_t)r * a.mask_stride + (e >> 5)] >> (e & 31u)) & 1u);
-                    visit(e, row_special_value(c, SL, e, raw_at<DT>(rp, e), cnt, bcode, ban, off));
+                    const float l = row_special_value(c, SL, e, raw_at<DT>(rp, e), cnt, bcode, ban, off);
+                    am_merge(tm, ta, l, isnan(l) ? NONE : e);
+                    if (gsum_on) gsum_add(l);
+                    if (cand_ok(l)) {
+                        const uint32_t slot = atomicAdd(&SL.wcn[wv], 1u);
+                        if (slot < CANDW) {
+                            candw[slot].id = e;
+                            candw[slot].l = l;
+                        }
+                    }
                 }
             }
         }
+    } else if (lane == 0) {
+        SL.wcn[wv] = wcand;
     }
 
     // row results: per-wave DPP reductions, merged by every thread
@@ -2209,7 +2347,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         SL.gm[wv] = wgm;
         SL.gs[wv] = wgs;
     }
-    __syncthreads();
+    lds_barrier();
     float m = SL.wm[0];
     uint32_t am = SL.wa[0];
 #pragma unroll
@@ -2222,16 +2360,38 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             if (isfinite(SL.gm[k])) gsum += (double)SL.gs[k] * exp((double)SL.gm[k] - (double)m);
     }
     uint32_t flags = sflags;
-    const uint32_t n = gather ? SL.ncand : 0u;
-    if (gather && n > FIN_CAP) flags |= CS_OVERFLOW;
+    uint32_t n = 0;
+    uint32_t pre[RWV];  // candidates before each wave's region
+#pragma unroll
+    for (int k = 0; k < RWV; ++k) {
+        pre[k] = n;
+        const uint32_t cw = gather ? SL.wcn[k] : 0u;
+        if (cw > CANDW) flags |= CS_OVERFLOW;
+        n += cw < CANDW ? cw : CANDW;
+    }
+    // the k-th candidate across the wave regions (unrolled selects: no
+    // dynamic indexing of registers)
+    auto cand_at = [&](uint32_t k) -> Cand {
+        uint32_t w = 0, base = 0;
+#pragma unroll
+        for (int q = 1; q < RWV; ++q)
+            if (k >= pre[q]) {
+                w = (uint32_t)q;
+                base = pre[q];
+            }
+        return (&SL.cand[0][0])[w * CANDW + (k - base)];
+    };
     if (gather && !(flags & (CS_ERROR | CS_OVERFLOW)) && am != NONE && isfinite(m) && n <= 256u) {
         // min-p row with few candidates: wave 0 decides alone
         if (wv != 0) return;
-        wave_decide_minp<RT>(a, r, c.p, m, inv, am, n, SL.v.cand, SL.u.F);
+        wave_decide_minp<RT>(a, r, c.p, m, inv, am, n, cand_at, (uint64_t*)SL.stage, SL.u.F, lnmin, urow);
         return;
     }
     finish_decide<RT>(a, r, c.p, m, am, flags, gsum, n, SL.u.F, [&](auto&& f) {
-        for (uint32_t i = tid; i < n; i += RT) f(SL.v.cand[i].id, SL.v.cand[i].l);
+        for (uint32_t i = tid; i < n; i += RT) {
+            const Cand cd = cand_at(i);
+            f(cd.id, cd.l);
+        }
     });
 }
 
