@@ -2112,11 +2112,11 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             traw = raw;
             tmw = mw;
         }
-        uint32_t qm = 0;  // the vector's min-p candidates
+        uint32_t qm = 0;  // the vector's min-p candidates (a superset of the survivors)
         if (gather && vm >= lpre) {
 #pragma unroll
             for (int q = 0; q < EPV; ++q)
-                if (v[q] >= lpre && __fmul_rn(__fsub_rn(v[q], mrun), inv) >= thr) qm |= 1u << q;
+                if (v[q] >= lpre) qm |= 1u << q;
         }
         if (gsum_on) {
 #pragma unroll
