@@ -907,10 +907,18 @@ __device__ __forceinline__ void decide_sorted(const KArgs& a, int r, const axs_s
     }
 }
 
-// Lists row r for the exact path (second pass over its logits) with its
-// maximum m.  One thread.
-__device__ __forceinline__ void list_exact(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
-                                           uint32_t mode, bool sorted, uint32_t am) {
+// A min-p row with no survivor (min_p > 1): argmax (sampling.rs:290-293).
+// One thread.
+__device__ __forceinline__ void empty_minp(const KArgs& a, int r, uint32_t am) {
+    const uint32_t flags = AXS_FLAG_ARGMAX_FALLBACK | AXS_FLAG_EXACT_PATH;
+    write_row(a, r, am, NAN, flags);
+    write_single_kept(a, r, am);
+    if (a.ws_kept_id) a.rstate[r].flags = flags;
+}
+
+// Row r's exact-path state from its maximum m (lowest id am).
+__device__ __forceinline__ RowState exact_state(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
+                                                uint32_t mode, bool sorted, uint32_t am) {
     const bool minp = mode == M_MINP;
     RowState rs;
     rs.m = m;
@@ -927,7 +935,14 @@ __device__ __forceinline__ void list_exact(const KArgs& a, int r, const axs_samp
     rs.F = 0.0f;
     rs.nlist = 0;
     rs.pad[0] = rs.pad[1] = rs.pad[2] = 0;
-    a.rstate[r] = rs;
+    return rs;
+}
+
+// Lists row r for the exact path (second pass over its logits) with its
+// maximum m.  One thread.
+__device__ __forceinline__ void list_exact(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
+                                           uint32_t mode, bool sorted, uint32_t am) {
+    a.rstate[r] = exact_state(a, r, p, m, inv, mode, sorted, am);
     const uint32_t idx = atomicAdd(a.exact_count, 1u);
     a.exact_rows[idx] = (uint32_t)r;
 }
@@ -936,12 +951,14 @@ __device__ __forceinline__ void list_exact(const KArgs& a, int r, const axs_samp
 // id am (NONE for an all-NaN row), the CS_* flags, gs = the sum of exp(l - m)
 // over finite l (greedy logprob), and cands(f), which calls f(id, l) for this
 // thread's share of the ncand gathered candidates (a superset of the ids that
-// survive min-p).  Rows it cannot decide are listed for the exact path.
+// survive min-p).  Rows it cannot decide are listed for the exact path, or,
+// with INPLACE, returned: true and their state in *xs, for the caller's
+// workgroup to take the exact path itself.
 // Called by all threads of the workgroup (uniform control flow).
-template <int NT, typename CF>
-__device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_sampling_params& p, float m,
+template <int NT, bool INPLACE = false, typename CF>
+__device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_sampling_params& p, float m,
                                               uint32_t am, uint32_t fl, double gs, uint32_t ncand,
-                                              FinLds<NT>& F, CF&& cands) {
+                                              FinLds<NT>& F, CF&& cands, RowState* xs = nullptr) {
     const int tid = threadIdx.x;
     const uint32_t mode = row_mode(p);
     if (am == NONE) {  // all-NaN row: argmax_f32 → 0 (sampling.rs:966)
@@ -958,7 +975,7 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
                 a.rstate[r].flags = AXS_FLAG_ERROR;
             }
         }
-        return;
+        return false;
     }
     if (mode == M_GREEDY) {
         if (tid == 0) {
@@ -967,7 +984,7 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
             write_single_kept(a, r, am);
             if (a.ws_kept_id) a.rstate[r].flags = AXS_FLAG_GREEDY;
         }
-        return;
+        return false;
     }
     const float inv = __fdiv_rn(1.0f, p.temperature);
     if (!(isfinite(m) && isfinite(inv))) {
@@ -977,7 +994,7 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
             write_single_kept(a, r, am);
             if (a.ws_kept_id) a.rstate[r].flags = AXS_FLAG_ARGMAX_FALLBACK;
         }
-        return;
+        return false;
     }
     const bool minp = mode == M_MINP;
     const bool sorted = minp ? filters_enabled(p) : (mode != M_FAST);
@@ -997,8 +1014,12 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
         });
         mg = -block_max<NT>(-mg, F.rf);
         const uint32_t n = F.n;
-        if (n == 0) exact = true;  // (unreachable: the maximum itself has p = 1)
-        if (!exact) {
+        if (n == 0) {
+            // min_p > 1: no survivor (sampling.rs:292)
+            if (tid == 0) empty_minp(a, r, am);
+            return false;
+        }
+        {
             const uint32_t flags0 = mg < 1e-6f ? AXS_FLAG_NEAR_MINP : 0u;
             constexpr uint32_t RS_MAX = 512;  // rank sort up to this many keys
             if (n <= RS_MAX) {
@@ -1032,7 +1053,14 @@ __device__ __forceinline__ void finish_decide(const KArgs& a, int r, const axs_s
             if (tid < 64) decide_sorted<NT>(a, r, p, mode, sorted, F, n, flags0, row_uniform(a, r, p));
         }
     }
-    if (exact && tid == 0) list_exact(a, r, p, m, inv, mode, sorted, am);
+    if (exact) {
+        if (INPLACE) {
+            *xs = exact_state(a, r, p, m, inv, mode, sorted, am);
+            return true;
+        }
+        if (tid == 0) list_exact(a, r, p, m, inv, mode, sorted, am);
+    }
+    return false;
 }
 
 // A min-p row decided by one wave from n <= 256 gathered candidates (a
@@ -1082,8 +1110,8 @@ __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const ax
         ns += (uint32_t)__popcll(bk);
     }
     const bool anynear = __ballot(near) != 0ull;
-    if (ns == 0) {  // (unreachable: the maximum itself has p = 1)
-        if (lane == 0) list_exact(a, r, p, m, inv, M_MINP, sorted, am);
+    if (ns == 0) {  // min_p > 1: no survivor
+        if (lane == 0) empty_minp(a, r, am);
         return;
     }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -1670,6 +1698,16 @@ constexpr uint32_t RERR_HASH = 1u;         // more special ids than hash slots
 constexpr uint32_t RERR_BIAS = 2u;         // more bias entries than RBCAP
 constexpr uint32_t RERR_CAP = 4u;          // a wave captured more than CAPW
 
+// LDS of the exact path's sort and running sums (one row per workgroup)
+struct ExLds {
+    uint32_t cnt[NBUCKET];  // bucket counts, then bucket ends; big-bucket sort scratch
+    Xd w[NT_EX / 64];
+    uint32_t u[NT_EX / 64];
+    float s;
+    uint32_t k, cross, nbig, err;
+    uint32_t big[256];
+};
+
 struct RowLds {
     union {
         struct {
@@ -1679,10 +1717,15 @@ struct RowLds {
         } p;
         FinLds<RT> F;
     } u;
-    Cand cand[RWV][CANDW];  // each wave's min-p candidates (ballot slots)
-    uint32_t wcn[RWV];      // their counts
-    uint32_t stage[HPRE];  // the window's first tokens (read by the hash build during the stream)
-    Cand cap[RWV][CAPW];
+    union {
+        struct {
+            Cand cand[RWV][CANDW];  // each wave's min-p candidates (ballot slots)
+            uint32_t stage[HPRE];   // the window's first tokens (read by the hash build during the stream)
+            Cand cap[RWV][CAPW];
+        };
+        ExLds ex;  // a row that takes the exact path in place (the above are dead by then)
+    };
+    uint32_t wcn[RWV];  // candidate counts
     uint32_t bias_id[RBCAP];
     float bias_v[RBCAP];
     u32x4 xt[256];
@@ -1691,6 +1734,7 @@ struct RowLds {
     float gm[RWV];      // per-wave greedy logprob partials: maximum ...
     float gs[RWV];      // ... and sum of exp(l - maximum)
     uint32_t next, nbias, err;
+    uint32_t xn;    // exact path in place: compacted keys
     uint32_t bpos;  // some bias entry is not <= 0 (it may raise a logit)
     int gmax;       // shared lower bound of the row maximum (ordered-int encoding)
 };
@@ -1768,6 +1812,8 @@ __device__ __forceinline__ float row_special_value(const RowCtx& c, const RowLds
     if (ban) l = -INFINITY;
     return l;
 }
+
+__device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState& rs, ExLds& X);
 
 template <int DT, int TV, bool MASK, bool FAST>
 __global__ __launch_bounds__(RT) void k_row(KArgs a) {
@@ -2387,12 +2433,113 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         wave_decide_minp<RT>(a, r, c.p, m, inv, am, n, cand_at, (uint64_t*)SL.stage, SL.u.F, lnmin, urow);
         return;
     }
-    finish_decide<RT>(a, r, c.p, m, am, flags, gsum, n, SL.u.F, [&](auto&& f) {
-        for (uint32_t i = tid; i < n; i += RT) {
-            const Cand cd = cand_at(i);
-            f(cd.id, cd.l);
+    RowState xs;
+    const bool ex = finish_decide<RT, true>(
+        a, r, c.p, m, am, flags, gsum, n, SL.u.F,
+        [&](auto&& f) {
+            for (uint32_t i = tid; i < n; i += RT) {
+                const Cand cd = cand_at(i);
+                f(cd.id, cd.l);
+            }
+        },
+        &xs);
+    if (!ex) return;
+
+    // The exact path in place (laws without min-p, candidate overflow): every
+    // element's probability with the row maximum, from a second read of the
+    // row (processors as in the stream: the bitmap and hash are intact), as a
+    // dense row (index-order laws) or compacted (p desc, id asc) keys at or
+    // above the floor (sorted laws); then exact_row sorts, sums and decides.
+    if (tid == 0) {
+        a.rstate[r] = xs;
+        SL.xn = 0;
+    }
+    const bool xminp = xs.mode == M_MINP;
+    const bool xsorted = xs.sorted != 0;
+    const bool hok = !(SL.err & RERR_HASH);
+    float* dense = a.dense + (size_t)r * a.vocab;
+    uint64_t* ck = a.ckey + (size_t)r * a.vocab;
+    float xmg = INFINITY;
+    auto xval = [&](uint32_t e, float raw, bool off) -> float {
+        uint32_t cnt, bcode;
+        bool ban;
+        if (hok) {
+            const uint32_t s = hash_find(SL.u.p.hkey, e);
+            const uint32_t hv = s == NONE ? 0u : SL.u.p.hval[s];
+            cnt = hv & HV_CNT;
+            bcode = (hv >> HV_BSH) & HV_BMULTI;
+            ban = (hv & HV_BAN) != 0u;
+        } else {
+            const uint32_t cw = count_word_hbm(a, c, e);
+            cnt = cw & ~CNT_BAN;
+            bcode = HV_BMULTI;
+            ban = (cw & CNT_BAN) != 0u;
         }
-    });
+        return row_special_value(c, SL, e, raw, cnt, bcode, ban, off);
+    };
+    lds_barrier();
+    constexpr int XV = 4;  // vectors per thread per tile
+    constexpr uint32_t XTILE = (uint32_t)RT * XV * EPV;
+    for (uint32_t t0 = 0; t0 < hi; t0 += XTILE) {
+        Tile<DT, XV, MASK> T;
+        tile_load<DT, XV, MASK, RT>(a, r, rp, t0, hi, (uint32_t)tid, T);
+#pragma unroll
+        for (int j = 0; j < XV; ++j) {
+            const uint32_t e0 = t0 + ((uint32_t)j * RT + (uint32_t)tid) * EPV;
+            const uint32_t mw = MASK ? T.mw[j] : 0xFFFFFFFFu;
+            const uint32_t sk = e0 < hi ? spec_bits(e0) : 0u;
+            float v[EPV];
+            vec_vals(T.raw[j], mw, e0, sk, v);
+            uint32_t km = 0;
+#pragma unroll
+            for (int q = 0; q < EPV; ++q) {
+                const uint32_t e = e0 + (uint32_t)q;
+                if ((sk >> q) & 1u) v[q] = xval(e, unpack<DT>(T.raw[j], q), MASK && !((mw >> (e & 31u)) & 1u));
+                const float pr = prob_of(v[q], xs.m, xs.inv);
+                bool keep = true;
+                if (xminp) {
+                    if (!isnan(v[q]) && e < hi) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
+                    keep = pr >= c.p.min_p;
+                }
+                v[q] = keep ? pr : 0.0f;
+                if (e < hi) {
+                    if (!xsorted) dense[e] = v[q];
+                    else if (v[q] >= xs.pmin) km |= 1u << q;
+                }
+            }
+            if (xsorted) {
+                // the wave's keys, at one LDS claim per vector
+                const uint32_t mine = (uint32_t)__popc(km);
+                uint32_t incl = mine;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const uint32_t y = (uint32_t)__shfl_up((int)incl, d, 64);
+                    if (lane >= d) incl += y;
+                }
+                const uint32_t tot = (uint32_t)__shfl((int)incl, 63, 64);
+                uint32_t base = 0;
+                if (lane == 0 && tot) base = atomicAdd(&SL.xn, tot);
+                uint32_t o = (uint32_t)__shfl((int)base, 0, 64) + incl - mine;
+#pragma unroll
+                for (int q = 0; q < EPV; ++q)
+                    if ((km >> q) & 1u) ck[o++] = key_pdesc(v[q], e0 + (uint32_t)q);
+            }
+        }
+    }
+    if (xminp) {
+        const float wmg = -wave_max_dpp(-xmg);
+        if (lane == 0) SL.wm[wv] = wmg;
+    }
+    __threadfence_block();
+    __syncthreads();  // the row's keys / probabilities are complete
+    if (xminp) {
+        float g = SL.wm[0];
+#pragma unroll
+        for (int k = 1; k < RWV; ++k) g = fminf(g, SL.wm[k]);
+        xs.minp_mg = __float_as_uint(g);
+    }
+    xs.ncompact = SL.xn;
+    exact_row(a, r, xs, SL.ex);
 }
 
 // --------------------------------------------------------------------------
@@ -2513,16 +2660,16 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t key) {
     return b < NBUCKET ? b : NBUCKET - 1;
 }
 
-__device__ void exact_row(const KArgs& a) {
-    __shared__ uint32_t s_cnt[NBUCKET];
-    __shared__ Xd s_w[NT_EX / 64];
-    __shared__ uint32_t s_u[NT_EX / 64];
-    __shared__ float s_s;
-    __shared__ uint32_t s_k, s_cross, s_nbig, s_err;
-    __shared__ uint32_t s_big[256];
+// Row r's exact path (rs: its state; X: LDS scratch).  Called by the NT_EX
+// threads of one workgroup.
+__device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState& rs, ExLds& XL) {
+    uint32_t* s_cnt = XL.cnt;
+    Xd* s_w = XL.w;
+    uint32_t* s_u = XL.u;
+    float& s_s = XL.s;
+    uint32_t &s_k = XL.k, &s_cross = XL.cross, &s_nbig = XL.nbig, &s_err = XL.err;
+    uint32_t* s_big = XL.big;
     const int tid = threadIdx.x;
-    const int r = (int)a.exact_rows[blockIdx.x];
-    const RowState rs = a.rstate[r];
     const axs_sampling_params p = row_params(a, r);
     const uint32_t V = (uint32_t)a.vocab;
     const bool sorted = rs.sorted != 0;
@@ -2770,6 +2917,10 @@ __device__ void exact_row(const KArgs& a) {
         if (kept == 0xFFFFFFFFu) kept = L;  // min-p survivors below 2^-24 are not listed
     } else {
         F = S[V - 1];
+        if (!(F > 0.0f)) {  // min_p > 1: no survivor (sampling.rs:290-293)
+            empty_minp(a, r, rs.amax);
+            return;
+        }
         const float thr = __fmul_rn(rs.u, F);
         uint32_t j = first_ge(S, 0, V, thr);
         if (j >= V) j = V - 1;
@@ -2821,8 +2972,13 @@ __device__ void exact_row(const KArgs& a) {
 // itself out; the last one clears the exact-row list for the next call (all
 // of them have read its length by then).
 __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
+    __shared__ ExLds X;
     const uint32_t nex = *a.exact_count;
-    if (blockIdx.x < nex) exact_row(a);
+    if (blockIdx.x < nex) {
+        const int r = (int)a.exact_rows[blockIdx.x];
+        const RowState rs = a.rstate[r];
+        exact_row(a, r, rs, X);
+    }
     __syncthreads();
     if (threadIdx.x == 0 && atomicInc(a.ex_done, gridDim.x - 1u) == gridDim.x - 1u) *a.exact_count = 0u;
 }
@@ -3232,6 +3388,7 @@ void launch_row(const KArgs& a, hipStream_t s) {
 // of MIN_CHUNK or the vocabulary, is then a multiple of the vector width)
 template <int DT>
 void launch_stream_dt(const Plan& pl, const KArgs& a, hipStream_t s) {
+    static_assert(RT == NT_EX, "k_row takes the exact path in place with its own workgroup");
     const bool fast = a.vec && a.vocab % (DT == AXS_DTYPE_BF16 ? 8 : 4) == 0;
     if (pl.wide) {
         if (fast) launch_row<DT, true>(a, s);
@@ -3308,6 +3465,10 @@ int run_pipeline(axs_context* c, KArgs& a, const Plan& pl, hipStream_t s) {
     if (rc) return rc;
     fill_ws(a, c);
     timed(c, AXS_KERNEL_STREAM, s, [&] { launch_stream(pl, a, s); });
+    if (pl.wide) {  // k_row takes the exact path in place
+        AXS_HIP_CHECK(hipGetLastError());
+        return AXS_OK;
+    }
     timed(c, AXS_KERNEL_EXACT_MAT, s, [&] { launch_exact_mat(pl, a, s); });
     timed(c, AXS_KERNEL_EXACT_ROW, s, [&] {
         hipLaunchKernelGGL(k_exact_row, dim3((unsigned)a.nrows), dim3(NT_EX), 0, s, a);
