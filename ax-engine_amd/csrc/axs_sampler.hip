@@ -1699,13 +1699,15 @@ constexpr uint32_t RERR_BIAS = 2u;         // more bias entries than RBCAP
 constexpr uint32_t RERR_CAP = 4u;          // a wave captured more than CAPW
 
 // LDS of the exact path's sort and running sums (one row per workgroup)
+constexpr uint32_t NMIXW = NBUCKET / 32;
 struct ExLds {
-    uint32_t cnt[NBUCKET];  // bucket counts, then bucket ends; big-bucket sort scratch
+    uint32_t cnt[NBUCKET];  // bucket counts, then bucket ends; then sort scratch
+    uint64_t stage[(NT_EX / 64) * 128];  // each wave's window of keys
+    uint32_t mixed[NMIXW];  // buckets of more than 64 keys with two different p
     Xd w[NT_EX / 64];
     uint32_t u[NT_EX / 64];
     float s;
-    uint32_t k, cross, nbig, err;
-    uint32_t big[256];
+    uint32_t k, cross, err;
 };
 
 struct RowLds {
@@ -2667,8 +2669,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     Xd* s_w = XL.w;
     uint32_t* s_u = XL.u;
     float& s_s = XL.s;
-    uint32_t &s_k = XL.k, &s_cross = XL.cross, &s_nbig = XL.nbig, &s_err = XL.err;
-    uint32_t* s_big = XL.big;
+    uint32_t &s_k = XL.k, &s_cross = XL.cross, &s_err = XL.err;
     const int tid = threadIdx.x;
     const axs_sampling_params p = row_params(a, r);
     const uint32_t V = (uint32_t)a.vocab;
@@ -2676,17 +2677,31 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     const uint32_t n = sorted ? rs.ncompact : V;
     const uint64_t* src = a.ckey + (size_t)r * V;
     uint64_t* keys = a.ckey2 + (size_t)r * V;
+    uint64_t* sorted_keys = a.ckey + (size_t)r * V;  // written once src is consumed
+    uint32_t* bend = a.bend + (size_t)r * NBUCKET;
     const float* dense = a.dense + (size_t)r * V;
     float* S = a.sbuf + (size_t)r * V;
-    if (tid == 0) {
-        s_err = 0;
-        s_nbig = 0;
-    }
+    if (tid == 0) s_err = 0;
+    // block sort of keys[st, en) by (p desc, id asc): in LDS (s_cnt) up to
+    // BIG_LDS_SORT keys, else in the row's HBM scratch.  Uniform control flow.
+    auto sort_range = [&](uint32_t st, uint32_t en) {
+        const uint32_t mcount = en - st;
+        if (mcount <= 1) return;
+        const uint32_t np2 = next_pow2(mcount);
+        uint64_t* t = np2 <= BIG_LDS_SORT ? (uint64_t*)s_cnt : a.tmp64 + (size_t)r * a.tmp_stride;
+        for (uint32_t i = tid; i < np2; i += NT_EX) t[i] = i < mcount ? keys[st + i] : 0ull;
+        __threadfence_block();
+        __syncthreads();
+        block_sort_desc<NT_EX>(t, np2);
+        for (uint32_t i = tid; i < mcount; i += NT_EX) keys[st + i] = t[i];
+        __threadfence_block();
+        __syncthreads();
+    };
 
     if (sorted) {
-        // counting sort by p bucket (descending p), then each bucket sorted
-        // by (p desc, id asc)
+        // counting sort by p bucket (descending p) into keys
         for (uint32_t i = tid; i < NBUCKET; i += NT_EX) s_cnt[i] = 0;
+        for (uint32_t i = tid; i < NMIXW; i += NT_EX) XL.mixed[i] = 0;
         __syncthreads();
         for (uint32_t i = tid; i < n; i += NT_EX) atomicAdd(&s_cnt[bucket_of(src[i])], 1u);
         __syncthreads();
@@ -2706,50 +2721,61 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             uint32_t pos = atomicAdd(&s_cnt[bucket_of(k)], 1u);
             keys[pos] = k;
         }
-        __syncthreads();
-        uint32_t* bend = a.bend + (size_t)r * NBUCKET;
-        for (uint32_t i = tid; i < NBUCKET; i += NT_EX) bend[i] = s_cnt[i];
         __threadfence_block();
         __syncthreads();
+        // s_cnt[b] is now the end of bucket b; kept in HBM for the phases
+        // that reuse s_cnt as sort scratch
+        for (uint32_t i = tid; i < NBUCKET; i += NT_EX) bend[i] = s_cnt[i];
+        // Each bucket of at most 64 keys is sorted by the wave whose window
+        // of 64 positions holds its start: the window's 128 keys staged in
+        // LDS, each key's rank = the keys of its bucket above it, written to
+        // sorted (the compaction array, free now).  Keys of larger buckets are
+        // copied in place, and a large bucket holding two different p is
+        // marked for a block sort; one whose p are all equal is already in p
+        // order, and its ids are ordered later only where an output reads
+        // them.
         const int wv = tid >> 6, lane = tid & 63;
-        for (uint32_t b = wv; b < NBUCKET; b += NT_EX / 64) {
-            uint32_t st = b ? bend[b - 1] : 0u, en = bend[b];
-            uint32_t mcount = en - st;
-            if (mcount <= 1) continue;
-            if (mcount <= 64) {
-                uint64_t k = lane < (int)mcount ? keys[st + lane] : 0ull;
-                k = wave_sort_desc(k);
-                if (lane < (int)mcount) keys[st + lane] = k;
-            } else if (lane == 0) {
-                uint32_t slot = atomicAdd(&s_nbig, 1u);
-                if (slot < 256) s_big[slot] = b;
-                else s_err = 1;
+        uint64_t* st = XL.stage + (uint32_t)wv * 128u;
+        for (uint32_t s0 = (uint32_t)wv * 64u; s0 < n; s0 += 64u * (NT_EX / 64)) {
+            const uint64_t k0 = s0 + (uint32_t)lane < n ? keys[s0 + lane] : 0ull;
+            const uint64_t k1 = s0 + 64u + (uint32_t)lane < n ? keys[s0 + 64u + lane] : 0ull;
+            st[lane] = k0;
+            st[64 + lane] = k1;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t pos = s0 + (uint32_t)h * 64u + (uint32_t)lane;
+                const uint64_t key = h ? k1 : k0;
+                if (pos >= n) continue;
+                const uint32_t b = bucket_of(key);
+                const uint32_t bs = b ? s_cnt[b - 1] : 0u, be = s_cnt[b];
+                if (be - bs <= 64u) {
+                    if (bs >= s0 && bs < s0 + 64u) {
+                        uint32_t rank = 0;
+                        for (uint32_t q = bs; q < be; ++q) rank += st[q - s0] > key ? 1u : 0u;
+                        sorted_keys[bs + rank] = key;
+                    }
+                } else {
+                    if (h == 0) sorted_keys[pos] = key;
+                    if (pdesc_p(key) != pdesc_p(keys[bs])) atomicOr(&XL.mixed[b >> 5], 1u << (b & 31u));
+                }
             }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
         }
         __threadfence_block();
         __syncthreads();
-        const uint32_t nbig = s_nbig < 256 ? s_nbig : 256;
-        uint64_t* lds = (uint64_t*)s_cnt;  // bucket counts no longer needed
-        for (uint32_t q = 0; q < nbig; ++q) {
-            uint32_t b = s_big[q];
-            uint32_t st = b ? bend[b - 1] : 0u, en = bend[b];
-            uint32_t mcount = en - st;
-            uint32_t np2 = next_pow2(mcount);
-            if (np2 <= BIG_LDS_SORT) {
-                for (uint32_t i = tid; i < np2; i += NT_EX) lds[i] = i < mcount ? keys[st + i] : 0ull;
-                __syncthreads();
-                block_sort_desc<NT_EX>(lds, np2);
-                for (uint32_t i = tid; i < mcount; i += NT_EX) keys[st + i] = lds[i];
-                __syncthreads();
-            } else {
-                uint64_t* t = a.tmp64 + (size_t)r * a.tmp_stride;
-                for (uint32_t i = tid; i < np2; i += NT_EX) t[i] = i < mcount ? keys[st + i] : 0ull;
-                __threadfence_block();
-                __syncthreads();
-                block_sort_desc<NT_EX>(t, np2);
-                for (uint32_t i = tid; i < mcount; i += NT_EX) keys[st + i] = t[i];
-                __threadfence_block();
-                __syncthreads();
+        keys = sorted_keys;
+        // large buckets with two different p: block sorts (uniform loop)
+        for (uint32_t wi = 0; wi < NMIXW; ++wi) {
+            uint32_t bits = XL.mixed[wi];
+            while (bits) {
+                const uint32_t b = wi * 32u + (uint32_t)__ffs((int)bits) - 1u;
+                bits &= bits - 1u;
+                sort_range(b ? bend[b - 1] : 0u, bend[b]);
             }
         }
     }
@@ -2865,8 +2891,8 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         dlist = base_w < cap_w ? base_w : cap_w;
     }
 
-    if (tid != 0) return;
-    // decisions (sampling.rs:283-316, 922-952) on the exact running sums
+    // decisions (sampling.rs:283-316, 922-952) on the exact running sums,
+    // computed by every thread (the same reads); one thread writes
     uint32_t flags = AXS_FLAG_DREW | AXS_FLAG_EXACT_PATH;
     if (s_err) flags |= AXS_FLAG_ERROR;
     const bool minp = rs.mode == M_MINP;
@@ -2875,11 +2901,13 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     float F = 0.0f, pj = 0.0f;
     uint32_t kept = 0, Lk = 0;
     if (n == 0) {
-        tok = rs.amax;
-        flags = AXS_FLAG_ARGMAX_FALLBACK | AXS_FLAG_EXACT_PATH;
-        write_row(a, r, tok, NAN, flags);
-        write_single_kept(a, r, tok);
-        if (a.ws_kept_id) a.rstate[r].flags = flags;
+        if (tid == 0) {
+            tok = rs.amax;
+            flags = AXS_FLAG_ARGMAX_FALLBACK | AXS_FLAG_EXACT_PATH;
+            write_row(a, r, tok, NAN, flags);
+            write_single_kept(a, r, tok);
+            if (a.ws_kept_id) a.rstate[r].flags = flags;
+        }
         return;
     }
     if (sorted) {
@@ -2912,13 +2940,27 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         double up = (double)S[j] - (double)thr;
         double lo = j > 0 ? (double)thr - (double)S[j - 1] : INFINITY;
         if (fmin(up, lo) / (double)F < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
+        // ids are read at the draw position and in the kept prefixes; a
+        // bucket of more than 64 keys with a single p is still in arbitrary
+        // id order, so each one holding such a position is sorted first
+        const uint32_t po = (a.out_kept && a.out_kept_cap > 0) ? min(Lk, (uint32_t)a.out_kept_cap) : 0u;
+        const uint32_t pw = a.ws_kept_id ? min(Lk, KEPT_CAP) : 0u;
+        const uint32_t P = max(po, pw);
+        auto order_ids = [&](uint32_t pos) -> uint32_t {  // returns the end of pos's bucket
+            const uint32_t b = bucket_of(keys[pos]);
+            const uint32_t bs = b ? bend[b - 1] : 0u, be = bend[b];
+            if (be - bs > 64u) sort_range(bs, be);
+            return be;
+        };
+        for (uint32_t pos = 0; pos < P;) pos = order_ids(pos);
+        if (j >= P) order_ids(j);
         tok = pdesc_id(keys[j]);
         pj = pdesc_p(keys[j]);
         if (kept == 0xFFFFFFFFu) kept = L;  // min-p survivors below 2^-24 are not listed
     } else {
         F = S[V - 1];
         if (!(F > 0.0f)) {  // min_p > 1: no survivor (sampling.rs:290-293)
-            empty_minp(a, r, rs.amax);
+            if (tid == 0) empty_minp(a, r, rs.amax);
             return;
         }
         const float thr = __fmul_rn(rs.u, F);
@@ -2931,6 +2973,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         pj = dense[j];
         kept = dkept;
     }
+    if (tid != 0) return;
     write_row(a, r, tok, logprob_of(__fdiv_rn(pj, F)), flags);
     if (a.out_kept_count) a.out_kept_count[r] = kept;
     if (a.out_kept && a.out_kept_cap > 0) {
