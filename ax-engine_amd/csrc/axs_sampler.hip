@@ -1815,6 +1815,7 @@ __device__ __forceinline__ float row_special_value(const RowCtx& c, const RowLds
     return l;
 }
 
+template <uint32_t XI>
 __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState& rs, ExLds& X);
 
 template <int DT, int TV, bool MASK, bool FAST>
@@ -2541,7 +2542,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         xs.minp_mg = __float_as_uint(g);
     }
     xs.ncompact = SL.xn;
-    exact_row(a, r, xs, SL.ex);
+    exact_row<4>(a, r, xs, SL.ex);
 }
 
 // --------------------------------------------------------------------------
@@ -2663,7 +2664,9 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t key) {
 }
 
 // Row r's exact path (rs: its state; X: LDS scratch).  Called by the NT_EX
-// threads of one workgroup.
+// threads of one workgroup; XI = keys or terms per thread in flight at once
+// (a register budget).
+template <uint32_t XI>
 __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState& rs, ExLds& XL) {
     uint32_t* s_cnt = XL.cnt;
     Xd* s_w = XL.w;
@@ -2703,7 +2706,15 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         for (uint32_t i = tid; i < NBUCKET; i += NT_EX) s_cnt[i] = 0;
         for (uint32_t i = tid; i < NMIXW; i += NT_EX) XL.mixed[i] = 0;
         __syncthreads();
-        for (uint32_t i = tid; i < n; i += NT_EX) atomicAdd(&s_cnt[bucket_of(src[i])], 1u);
+        constexpr uint32_t U = XI;  // keys per thread per round, every load issued first
+        for (uint32_t i0 = tid; i0 < n; i0 += NT_EX * U) {
+            uint64_t kk[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) kk[u] = i0 + u * NT_EX < n ? src[i0 + u * NT_EX] : 0ull;
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u)
+                if (i0 + u * NT_EX < n) atomicAdd(&s_cnt[bucket_of(kk[u])], 1u);
+        }
         __syncthreads();
         constexpr uint32_t PER = NBUCKET / NT_EX;
         uint32_t loc = 0;
@@ -2716,10 +2727,13 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             pre += c;
         }
         __syncthreads();
-        for (uint32_t i = tid; i < n; i += NT_EX) {
-            uint64_t k = src[i];
-            uint32_t pos = atomicAdd(&s_cnt[bucket_of(k)], 1u);
-            keys[pos] = k;
+        for (uint32_t i0 = tid; i0 < n; i0 += NT_EX * U) {
+            uint64_t kk[U];
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u) kk[u] = i0 + u * NT_EX < n ? src[i0 + u * NT_EX] : 0ull;
+#pragma unroll
+            for (uint32_t u = 0; u < U; ++u)
+                if (i0 + u * NT_EX < n) keys[atomicAdd(&s_cnt[bucket_of(kk[u])], 1u)] = kk[u];
         }
         __threadfence_block();
         __syncthreads();
@@ -2736,9 +2750,13 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         // them.
         const int wv = tid >> 6, lane = tid & 63;
         uint64_t* st = XL.stage + (uint32_t)wv * 128u;
-        for (uint32_t s0 = (uint32_t)wv * 64u; s0 < n; s0 += 64u * (NT_EX / 64)) {
-            const uint64_t k0 = s0 + (uint32_t)lane < n ? keys[s0 + lane] : 0ull;
-            const uint64_t k1 = s0 + 64u + (uint32_t)lane < n ? keys[s0 + 64u + lane] : 0ull;
+        constexpr uint32_t WSTEP = 64u * (NT_EX / 64);
+        auto wload = [&](uint32_t at) { return at < n ? keys[at] : 0ull; };
+        uint64_t n0 = wload((uint32_t)wv * 64u + lane), n1 = wload((uint32_t)wv * 64u + 64u + lane);
+        for (uint32_t s0 = (uint32_t)wv * 64u; s0 < n; s0 += WSTEP) {
+            const uint64_t k0 = n0, k1 = n1;
+            n0 = wload(s0 + WSTEP + lane);  // the next window's keys, in flight meanwhile
+            n1 = wload(s0 + WSTEP + 64u + lane);
             st[lane] = k0;
             st[64 + lane] = k1;
             __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -2753,8 +2771,14 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
                 const uint32_t bs = b ? s_cnt[b - 1] : 0u, be = s_cnt[b];
                 if (be - bs <= 64u) {
                     if (bs >= s0 && bs < s0 + 64u) {
-                        uint32_t rank = 0;
-                        for (uint32_t q = bs; q < be; ++q) rank += st[q - s0] > key ? 1u : 0u;
+                        uint32_t rank = 0, q = bs;
+                        for (; q + 4u <= be; q += 4u) {  // four LDS reads in flight
+                            const uint64_t c0 = st[q - s0], c1 = st[q + 1u - s0];
+                            const uint64_t c2 = st[q + 2u - s0], c3 = st[q + 3u - s0];
+                            rank += (c0 > key ? 1u : 0u) + (c1 > key ? 1u : 0u) + (c2 > key ? 1u : 0u) +
+                                    (c3 > key ? 1u : 0u);
+                        }
+                        for (; q < be; ++q) rank += st[q - s0] > key ? 1u : 0u;
                         sorted_keys[bs + rank] = key;
                     }
                 } else {
@@ -2770,6 +2794,9 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         __syncthreads();
         keys = sorted_keys;
         // large buckets with two different p: block sorts (uniform loop)
+        uint32_t anym = 0;
+        for (uint32_t i = tid; i < NMIXW; i += NT_EX) anym |= XL.mixed[i];
+        if (__syncthreads_or(anym != 0u))
         for (uint32_t wi = 0; wi < NMIXW; ++wi) {
             uint32_t bits = XL.mixed[wi];
             while (bits) {
@@ -2788,7 +2815,12 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         s_k = 0;
     }
     __syncthreads();
-    constexpr uint32_t IT = 4;
+    // Each round: a tile of IT terms per thread, all in the binade of the
+    // current sum; the first term that would leave it (the earliest crossing
+    // over the block) is added directly by its thread, which sets the next
+    // round's start.  The round's state stays in LDS.
+    constexpr uint32_t IT = XI;
+    if (tid == 0) s_cross = NONE;
     while (true) {
         const float s = s_s;
         const uint32_t k = s_k;
@@ -2796,13 +2828,15 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         const Binade bd = binade_of(s);
         const uint32_t tile = min((uint32_t)NT_EX * IT, n - k);
         const uint32_t i0 = k + (uint32_t)tid * IT;
+        float xv[IT];
         Term t[IT];
         Xd mine = xd_identity();
 #pragma unroll
+        for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
+#pragma unroll
         for (uint32_t j = 0; j < IT; ++j) {
-            uint32_t i = i0 + j;
-            if (i < k + tile) {
-                t[j] = term_of(X(i), bd.E);
+            if (i0 + j < k + tile) {
+                t[j] = term_of(xv[j], bd.E);
                 mine = xd_compose(mine, xd_of(t[j]));
             }
         }
@@ -2811,39 +2845,39 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
         uint32_t par = b0 ? pre.par1 : pre.par0;
         uint32_t mycross = NONE;
+        float xs = 0.0f, last = 0.0f;
 #pragma unroll
         for (uint32_t j = 0; j < IT; ++j) {
-            uint32_t i = i0 + j;
+            const uint32_t i = i0 + j;
             if (i >= k + tile || mycross != NONE) continue;
-            uint32_t cc = par ? t[j].c1 : t[j].c0;
+            const uint32_t cc = par ? t[j].c1 : t[j].c0;
             if (acc + cc >= (1ull << 24)) {
                 mycross = i;
+                xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
                 continue;
             }
             acc += cc;
             par = (uint32_t)(acc & 1u);
-            S[i] = binade_value((uint32_t)acc, bd.E);
+            last = binade_value((uint32_t)acc, bd.E);
+            S[i] = last;
         }
-        if (tid == 0) s_cross = NONE;
-        __syncthreads();
         if (mycross != NONE) atomicMin(&s_cross, mycross);
         __threadfence_block();
         __syncthreads();
-        if (tid == 0) {
-            const uint32_t kc = s_cross;
-            if (kc == NONE) {
-                s_s = S[k + tile - 1];
+        const uint32_t kc = s_cross;
+        if (kc == NONE) {
+            if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last term
+                s_s = last;
                 s_k = k + tile;
-            } else {
-                float prev = kc == k ? s : S[kc - 1];
-                float ns = __fadd_rn(prev, X(kc));
-                S[kc] = ns;
-                s_s = ns;
-                s_k = kc + 1;
             }
+        } else if (mycross == kc) {
+            S[kc] = xs;
+            s_s = xs;
+            s_k = kc + 1u;
         }
         __threadfence_block();
         __syncthreads();
+        if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
     }
 
     // index-order rows: the kept-set size and the ordered kept lists, by the
@@ -2973,29 +3007,29 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         pj = dense[j];
         kept = dkept;
     }
+    // the ordered kept lists (every thread)
+    if (sorted && a.out_kept && a.out_kept_cap > 0) {
+        // kept entries below the compaction floor (p < 2^-24 of the
+        // maximum's: never drawn) are not ordered here; they are listed as
+        // NONE after the ordered prefix
+        const uint32_t cap = (uint32_t)a.out_kept_cap;
+        const uint32_t nw = Lk < cap ? Lk : cap;
+        const uint32_t ne = kept < cap ? kept : cap;
+        for (uint32_t i = tid; i < ne; i += NT_EX) a.out_kept[(size_t)r * cap + i] = i < nw ? pdesc_id(keys[i]) : NONE;
+    }
+    const uint32_t nws = Lk < KEPT_CAP ? Lk : KEPT_CAP;
+    if (sorted && a.ws_kept_id)
+        for (uint32_t i = tid; i < nws; i += NT_EX) {
+            a.ws_kept_id[(size_t)r * KEPT_CAP + i] = pdesc_id(keys[i]);
+            a.ws_kept_p[(size_t)r * KEPT_CAP + i] = pdesc_p(keys[i]);
+        }
     if (tid != 0) return;
     write_row(a, r, tok, logprob_of(__fdiv_rn(pj, F)), flags);
     if (a.out_kept_count) a.out_kept_count[r] = kept;
-    if (a.out_kept && a.out_kept_cap > 0) {
-        uint32_t cap = (uint32_t)a.out_kept_cap;
-        if (sorted) {
-            // kept entries below the compaction floor (p < 2^-24 of the
-            // maximum's: never drawn) are not ordered here; they are listed
-            // as NONE after the ordered prefix
-            uint32_t nw = Lk < cap ? Lk : cap;
-            for (uint32_t i = 0; i < nw; ++i) a.out_kept[(size_t)r * cap + i] = pdesc_id(keys[i]);
-            const uint32_t ne = kept < cap ? kept : cap;
-            for (uint32_t i = nw; i < ne; ++i) a.out_kept[(size_t)r * cap + i] = NONE;
-        }
-    }
     if (a.ws_kept_id) {
         uint32_t o = 0;
         if (sorted) {
-            for (uint32_t i = 0; i < Lk && o < KEPT_CAP; ++i) {
-                a.ws_kept_id[(size_t)r * KEPT_CAP + o] = pdesc_id(keys[i]);
-                a.ws_kept_p[(size_t)r * KEPT_CAP + o] = pdesc_p(keys[i]);
-                ++o;
-            }
+            o = nws;
             // ids below 2^-24 never carry normalised mass ≥ one f32 ulp of 1, but
             // they are entries of the reference's distribution: refuse to
             // truncate silently
@@ -3020,7 +3054,7 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
     if (blockIdx.x < nex) {
         const int r = (int)a.exact_rows[blockIdx.x];
         const RowState rs = a.rstate[r];
-        exact_row(a, r, rs, X);
+        exact_row<8>(a, r, rs, X);
     }
     __syncthreads();
     if (threadIdx.x == 0 && atomicInc(a.ex_done, gridDim.x - 1u) == gridDim.x - 1u) *a.exact_count = 0u;
@@ -3030,12 +3064,17 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
 // k_mtp_verify: accept / residual / bonus per sequence
 // (crates/ax-engine-mlx/src/runner/mod.rs:12388-12431, sampling.rs:709-752)
 // --------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void k_mtp_verify(KArgs a, const uint32_t* draft_ids,
-                                                    uint32_t* out_ids, uint32_t* out_count,
-                                                    uint32_t* out_accept, uint32_t* out_flags) {
+constexpr int NT_MTP = 1024;
+__global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* draft_ids,
+                                                       uint32_t* out_ids, uint32_t* out_count,
+                                                       uint32_t* out_accept, uint32_t* out_flags) {
     __shared__ uint64_t s_t[KEPT_CAP];
     __shared__ uint64_t s_d[KEPT_CAP];
+    __shared__ float s_v[KEPT_CAP];     // residual terms (then their normalised values) in walk order
+    __shared__ uint32_t s_id[KEPT_CAP]; // ... and their ids
     __shared__ int s_ft, s_fd;
+    __shared__ float s_rsum;
+    __shared__ uint32_t s_rn;
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int D = a.mtp_depth;
@@ -3068,9 +3107,9 @@ __global__ __launch_bounds__(256) void k_mtp_verify(KArgs a, const uint32_t* dra
             s_fd = -1;
         }
         __syncthreads();
-        for (uint32_t k = tid; k < rt.nlist; k += 256)
+        for (uint32_t k = tid; k < rt.nlist; k += NT_MTP)
             if (tid_l[k] == d) atomicMax(&s_ft, (int)k);
-        for (uint32_t k = tid; k < rd.nlist; k += 256)
+        for (uint32_t k = tid; k < rd.nlist; k += NT_MTP)
             if (did_l[k] == d) atomicMax(&s_fd, (int)k);
         __syncthreads();
         // normalised entries p / F (TokenDistribution::new, sampling.rs:128-144)
@@ -3093,95 +3132,89 @@ __global__ __launch_bounds__(256) void k_mtp_verify(KArgs a, const uint32_t* dra
             continue;
         }
         // residual max(P - Q, 0) over the union of ids, ascending id order
+        // (runner/mod.rs:12409-12431, sampling.rs:709-752).  An id only in
+        // the draft carries max(0 - q, 0) = 0 and is skipped, so the walk is
+        // over the target's ids: both lists sorted by id, each target term
+        // with its draft entry found by binary search, all in parallel; the
+        // reference's sequential f32 sums run on one thread over LDS.
         const float ut = a.uniforms ? a.uniforms[(size_t)b * (D + 1) + D]
                                     : philox_uniform(tp.seed, (uint32_t)b, tp.step,
                                                      1u + (uint32_t)D / 4u, (uint32_t)D & 3u);
         const uint32_t nt = rt.nlist, nd = rd.nlist;
         uint32_t npt = next_pow2(nt > 0 ? nt : 1), npd = next_pow2(nd > 0 ? nd : 1);
-        for (uint32_t k = tid; k < npt; k += 256)
-            s_t[k] = k < nt ? (((uint64_t)(~tid_l[k]) << 32) |
-                               __float_as_uint(__fdiv_rn(tp_l[k], rt.F)))
-                            : 0ull;
-        for (uint32_t k = tid; k < npd; k += 256)
-            s_d[k] = k < nd ? (((uint64_t)(~did_l[k]) << 32) |
-                               __float_as_uint(__fdiv_rn(dp_l[k], rd.F)))
-                            : 0ull;
+        for (uint32_t k = tid; k < npt; k += NT_MTP)
+            s_t[k] = k < nt ? (((uint64_t)(~tid_l[k]) << 32) | __float_as_uint(__fdiv_rn(tp_l[k], rt.F))) : 0ull;
+        for (uint32_t k = tid; k < npd; k += NT_MTP)
+            s_d[k] = k < nd ? (((uint64_t)(~did_l[k]) << 32) | __float_as_uint(__fdiv_rn(dp_l[k], rd.F))) : 0ull;
         __syncthreads();
-        block_sort_desc<256>(s_t, npt);  // descending ~id = ascending id
-        block_sort_desc<256>(s_d, npd);
+        block_sort_desc<NT_MTP>(s_t, npt);  // descending ~id = ascending id
+        block_sort_desc<NT_MTP>(s_d, npd);
+        for (uint32_t k = tid; k < nt; k += NT_MTP) {
+            const uint32_t id = idasc_id(s_t[k]);
+            uint32_t lo = 0, hi = nd;
+            while (lo < hi) {
+                const uint32_t mid = (lo + hi) >> 1;
+                if (idasc_id(s_d[mid]) < id) lo = mid + 1u;
+                else hi = mid;
+            }
+            const float ptk = idasc_p(s_t[k]);
+            s_v[k] = (lo < nd && idasc_id(s_d[lo]) == id) ? fmaxf(__fsub_rn(ptk, idasc_p(s_d[lo])), 0.0f) : ptk;
+            s_id[k] = id;
+        }
+        __syncthreads();
         if (tid == 0) {
-            // pass 1: residual sum in ascending id order
-            auto merged = [&](auto&& visit) {
-                uint32_t x = 0, y = 0;
-                while (x < nt || y < nd) {
-                    uint32_t ix = x < nt ? idasc_id(s_t[x]) : NONE;
-                    uint32_t iy = y < nd ? idasc_id(s_d[y]) : NONE;
-                    float v;
-                    if (ix == iy) {
-                        v = fmaxf(__fsub_rn(idasc_p(s_t[x]), idasc_p(s_d[y])), 0.0f);
-                        visit(ix, v);
-                        ++x;
-                        ++y;
-                    } else if (ix < iy) {
-                        v = idasc_p(s_t[x]);
-                        visit(ix, v);
-                        ++x;
-                    } else {
-                        ++y;  // only in the draft: max(0 - q, 0) = 0
-                    }
-                }
-            };
             float rsum = 0.0f;
             uint32_t rn = 0;
-            merged([&](uint32_t, float v) {
+            for (uint32_t k = 0; k < nt; ++k) {
+                const float v = s_v[k];
                 if (v > 0.0f && isfinite(v)) {
                     rsum = __fadd_rn(rsum, v);
                     ++rn;
                 }
-            });
-            uint32_t corr = NONE;
-            if (rn > 0 && rsum > 0.0f && isfinite(rsum)) {
-                // normalised residual, then sample_from_token_distribution
-                float total = 0.0f;
-                merged([&](uint32_t, float v) {
-                    if (v > 0.0f && isfinite(v)) total = __fadd_rn(total, __fdiv_rn(v, rsum));
-                });
-                float thr = __fmul_rn(ut, total);
-                float cum = 0.0f;
-                uint32_t last_id = NONE;
-                float bp = -1.0f;
-                merged([&](uint32_t id, float v) {
-                    if (!(v > 0.0f && isfinite(v)) || corr != NONE) return;
-                    float q = __fdiv_rn(v, rsum);
-                    cum = __fadd_rn(cum, q);
-                    if (q >= bp) {
-                        bp = q;
-                        last_id = id;
-                    }
-                    if (cum >= thr) corr = id;
-                });
-                if (corr == NONE) corr = last_id;
-            } else {
-                // empty residual: the target itself (sampling.rs:749)
-                float total = 0.0f;
-                for (uint32_t k = 0; k < nt; ++k) total = __fadd_rn(total, __fdiv_rn(tp_l[k], rt.F));
-                float thr = __fmul_rn(ut, total);
-                float cum = 0.0f, bp = -1.0f;
-                uint32_t last_id = NONE;
-                for (uint32_t k = 0; k < nt; ++k) {
-                    float q = __fdiv_rn(tp_l[k], rt.F);
-                    cum = __fadd_rn(cum, q);
-                    if (q >= bp) {
-                        bp = q;
-                        last_id = tid_l[k];
-                    }
-                    if (cum >= thr) {
-                        corr = tid_l[k];
-                        break;
-                    }
-                }
-                if (corr == NONE) corr = last_id;
             }
+            s_rsum = rsum;
+            s_rn = rn;
+        }
+        __syncthreads();
+        const float rsum = s_rsum;
+        uint32_t nw = nt;  // terms of the walk (s_v: value, or -1 for a skipped id)
+        if (s_rn > 0 && rsum > 0.0f && isfinite(rsum)) {
+            // normalised residual, then sample_from_token_distribution
+            for (uint32_t k = tid; k < nt; k += NT_MTP) {
+                const float v = s_v[k];
+                s_v[k] = (v > 0.0f && isfinite(v)) ? __fdiv_rn(v, rsum) : -1.0f;
+            }
+        } else {
+            // empty residual: the target itself, in its kept order (sampling.rs:749)
+            for (uint32_t k = tid; k < nt; k += NT_MTP) {
+                s_v[k] = __fdiv_rn(tp_l[k], rt.F);
+                s_id[k] = tid_l[k];
+            }
+        }
+        __syncthreads();
+        if (tid == 0) {
+            float total = 0.0f;
+            for (uint32_t k = 0; k < nw; ++k) {
+                const float q = s_v[k];
+                if (!(q < 0.0f)) total = __fadd_rn(total, q);
+            }
+            const float thr = __fmul_rn(ut, total);
+            float cum = 0.0f, bp = -1.0f;
+            uint32_t last_id = NONE, corr = NONE;
+            for (uint32_t k = 0; k < nw; ++k) {
+                const float q = s_v[k];
+                if (q < 0.0f) continue;
+                cum = __fadd_rn(cum, q);
+                if (q >= bp) {
+                    bp = q;
+                    last_id = s_id[k];
+                }
+                if (cum >= thr) {
+                    corr = s_id[k];
+                    break;
+                }
+            }
+            if (corr == NONE) corr = last_id;
             out_ids[(size_t)b * (D + 1) + count] = corr;
         }
         ++count;
@@ -3696,7 +3729,7 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_output
     int rc = run_pipeline(ctx, a, pl, s);
     if (rc) return rc;
     timed(ctx, AXS_KERNEL_MTP, s, [&] {
-        hipLaunchKernelGGL(k_mtp_verify, dim3((unsigned)d->batch), dim3(256), 0, s, a, d->draft_ids,
+        hipLaunchKernelGGL(k_mtp_verify, dim3((unsigned)d->batch), dim3(NT_MTP), 0, s, a, d->draft_ids,
                            o->out_ids, o->out_count, o->accept_count, o->flags);
     });
     AXS_HIP_CHECK(hipGetLastError());
