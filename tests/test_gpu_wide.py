@@ -104,3 +104,22 @@ def test_hash_overflow_fallback(sampler, oracle):
     gpu = run_gpu(sampler, w, us, kept_cap=64)
     cpu = run_oracle(oracle, w, us, kept_cap=64)
     log(f"hash overflow: {compare(w, gpu, cpu, 'hash-overflow')}")
+
+
+@pytest.mark.parametrize("B", [256, 16])
+def test_min_p_above_one(sampler, oracle, B):
+    """min_p > 1 leaves no survivor (the maximum has p = 1): argmax, no draw
+    (sampling.rs:290-293), for every draw law, on both the one-row-per-
+    workgroup shape (B = 256) and the segmented one (B = 16)."""
+    w = make_c3(8, B=B, V=65536)
+    rng = np.random.default_rng(88)
+    w.params["min_p"] = rng.choice(np.array([1.5, 0.05, 2.0], np.float32), B)
+    w.params["top_k"] = rng.choice(np.array([0, 40], np.uint32), B)
+    w.params["top_p"] = rng.choice(np.array([1.0, 0.9], np.float32), B)
+    us = _uniforms(w.B, 808)
+    gpu = run_gpu(sampler, w, us, kept_cap=8)
+    cpu = run_oracle(oracle, w, us, kept_cap=8)
+    log(f"min_p > 1, B={B}: {compare(w, gpu, cpu, f'minp-above-one-{B}')}")
+    big = w.params["min_p"] > 1.0
+    assert np.array_equal(gpu[0][big], cpu[0][big])
+    assert not np.any(gpu[2][big] & np.uint32(0x4)), "a row without survivors consumed a uniform"
