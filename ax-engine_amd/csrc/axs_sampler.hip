@@ -1066,17 +1066,19 @@ __device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_s
 // A min-p row decided by one wave from n <= 256 gathered candidates (a
 // superset of its min-p survivors, sampling.rs:283-294): survivors p =
 // exp((l - m) / T) >= min_p, ordered by (p desc, id asc) — or by id for an
-// index-order draw — then decide_sorted.  A candidate whose (l - m) / T is
-// more than 1e-5 from ln(min_p) is classified without its exact exp (rounding
-// moves exp by < 2^-24 relative); survivors get the correctly rounded one.
-// The survivors' keys are compacted by ballot into kbuf (LDS scratch of 256
-// keys, free once the candidates are read), then ranked (at most 64) or
-// bitonic-sorted.  cand_at(k) is the k-th candidate; lnmin = ln(min_p) and u
-// the row's uniform.  Called by the 64 lanes of one wave; no block barriers.
+// index-order draw — then decide_sorted.  x = (l - m) / T survives iff
+// x >= xstar, the smallest f32 whose correctly rounded exp reaches min_p (exp
+// is monotone), so only survivors need their exp: after the ballot
+// compaction into kbuf (LDS scratch of 256 keys, free once the candidates are
+// read) each lane computes its survivors' in parallel.  Candidates within
+// 1e-5 of ln(min_p) also get theirs, for the boundary flag.  The keys are then
+// ranked (each key's rank = the keys above it, read as LDS broadcasts).
+// cand_at(k) is the k-th candidate; lnmin = ln(min_p) and u the row's
+// uniform.  Called by the 64 lanes of one wave; no block barriers.
 template <int NT, typename CA>
 __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const axs_sampling_params& p, float m, float inv,
                                                  uint32_t am, uint32_t n, CA&& cand_at, uint64_t* kbuf,
-                                                 FinLds<NT>& F, double lnmin, float u) {
+                                                 FinLds<NT>& F, double lnmin, float xstar, float u) {
     const int lane = threadIdx.x & 63;
     const bool sorted = filters_enabled(p);
     Cand mine[4];
@@ -1093,20 +1095,16 @@ __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const ax
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         bool keep = false;
-        uint64_t key = 0;
+        uint64_t xk = 0;
         if (mine[j].id != NONE) {
             const float x = __fmul_rn(__fsub_rn(mine[j].l, m), inv);
+            keep = x >= xstar;
             const double dx = (double)x - lnmin;
-            float pr = 0.0f;
-            if (dx >= -1e-5) {
-                pr = prob_of(mine[j].l, m, inv);
-                keep = pr >= p.min_p;
-                if (dx <= 1e-5) near |= fabsf(pr - p.min_p) / p.min_p < 1e-6f;
-            }
-            if (keep) key = sorted ? key_pdesc(pr, mine[j].id) : key_idasc(pr, mine[j].id);
+            if (dx >= -1e-5 && dx <= 1e-5) near |= fabsf(prob_of(mine[j].l, m, inv) - p.min_p) / p.min_p < 1e-6f;
+            xk = ((uint64_t)__float_as_uint(x) << 32) | mine[j].id;
         }
         const uint64_t bk = __ballot(keep);
-        if (keep) kbuf[ns + mbcnt64(bk)] = key;
+        if (keep) kbuf[ns + mbcnt64(bk)] = xk;
         ns += (uint32_t)__popcll(bk);
     }
     const bool anynear = __ballot(near) != 0ull;
@@ -1117,24 +1115,39 @@ __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const ax
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // keys are distinct; survivors' keys are > 0
-    if (ns <= 64) {
-        const uint64_t my = (uint32_t)lane < ns ? kbuf[lane] : 0ull;
-        uint32_t rank = 0;
-        for (uint32_t j = 0; j < ns; ++j) rank += kbuf[j] > my ? 1u : 0u;
-        if ((uint32_t)lane < ns) F.key[rank] = my;
-    } else {
-        uint64_t k[4];
+    // the survivors' keys: their probabilities, every lane at once
+    const uint32_t nq = (ns + 63u) >> 6;  // keys per lane (uniform)
+    uint64_t my[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const uint32_t i = (uint32_t)lane + 64u * (uint32_t)j;
-            k[j] = i < ns ? kbuf[i] : 0ull;
+    for (int q = 0; q < 4; ++q) {
+        const uint32_t i = (uint32_t)lane + 64u * (uint32_t)q;
+        my[q] = 0ull;
+        if (i < ns) {
+            const uint64_t xk = kbuf[i];
+            const float pr = prob_of(__uint_as_float((uint32_t)(xk >> 32)), 0.0f, 1.0f);  // exp_cr(x): x - 0, * 1 exact
+            my[q] = sorted ? key_pdesc(pr, (uint32_t)xk) : key_idasc(pr, (uint32_t)xk);
         }
-        wave_sort_desc4(k);
-#pragma unroll
-        for (int j = 0; j < 4; ++j)
-            if ((uint32_t)lane + 64u * (uint32_t)j < ns) F.key[lane + 64 * j] = k[j];
     }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if ((uint32_t)lane + 64u * (uint32_t)q < ns) kbuf[lane + 64 * q] = my[q];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // rank = the keys above (keys are distinct), read as LDS broadcasts
+    uint32_t rk[4] = {0u, 0u, 0u, 0u};
+    for (uint32_t j = 0; j < ns; ++j) {
+        const uint64_t kj = kbuf[j];
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+            if ((uint32_t)q < nq) rk[q] += kj > my[q] ? 1u : 0u;
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+        if ((uint32_t)lane + 64u * (uint32_t)q < ns) F.key[rk[q]] = my[q];
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
@@ -1686,8 +1699,9 @@ constexpr int HWAVES = 2;              // waves that fetch the window before the
 constexpr uint32_t HPRE = 2048;        // window tokens staged through LDS
 constexpr uint32_t HBITS = 12;
 constexpr uint32_t HSZ = 1u << HBITS;  // hash slots
-constexpr uint32_t CAPW = 256;         // captured special elements per wave
-constexpr uint32_t CANDW = 256;        // min-p candidates per wave
+constexpr uint32_t CAPP = 2048;        // captured special elements per row (shared pool)
+constexpr uint32_t CANDP = 2048;       // min-p candidates per row (shared pool)
+constexpr uint32_t QN = 64;            // relevant vectors a wave queues before looking at them
 constexpr uint32_t RBCAP = 1024;       // bias entries per row
 constexpr uint32_t HV_CNT = 0x000FFFFFu;  // window count
 constexpr uint32_t HV_BSH = 20;           // bias entry index + 1, or HV_BMULTI
@@ -1696,7 +1710,7 @@ constexpr uint32_t HV_BAN = 0x80000000u;
 constexpr uint32_t CAP_OFF = 0x80000000u;  // captured element is masked off
 constexpr uint32_t RERR_HASH = 1u;         // more special ids than hash slots
 constexpr uint32_t RERR_BIAS = 2u;         // more bias entries than RBCAP
-constexpr uint32_t RERR_CAP = 4u;          // a wave captured more than CAPW
+constexpr uint32_t RERR_CAP = 4u;          // more than CAPP captures
 
 // LDS of the exact path's sort and running sums (one row per workgroup)
 constexpr uint32_t NMIXW = NBUCKET / 32;
@@ -1721,13 +1735,16 @@ struct RowLds {
     } u;
     union {
         struct {
-            Cand cand[RWV][CANDW];  // each wave's min-p candidates (ballot slots)
+            Cand cand[CANDP];       // min-p candidates (a wave claims a run of slots per batch)
             uint32_t stage[HPRE];   // the window's first tokens (read by the hash build during the stream)
-            Cand cap[RWV][CAPW];
+            Cand cap[CAPP];         // captured special elements (likewise)
+            u32x4 qraw[RWV][QN];    // each wave's queue of relevant vectors ...
+            uint32_t qe0[RWV][QN];  // ... their first ids ...
+            uint32_t qmw[RWV][QN];  // ... and mask words
         };
         ExLds ex;  // a row that takes the exact path in place (the above are dead by then)
     };
-    uint32_t wcn[RWV];  // candidate counts
+    uint32_t ncand, ncap;  // pool claims (may exceed the pools: overflow)
     uint32_t bias_id[RBCAP];
     float bias_v[RBCAP];
     u32x4 xt[256];
@@ -1746,6 +1763,24 @@ __device__ __forceinline__ int f2ord(float f) {
     return k >= 0 ? k : k ^ 0x7FFFFFFF;
 }
 __device__ __forceinline__ float ord2f(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF); }
+
+// The smallest f32 x with exp_cr(x) >= min_p (+inf when none, min_p > 1):
+// ln(min_p) rounded, moved by ulps; where exp rounds to the same value over
+// many ulps (near 0), a bisection over the ordered encoding of [-FLT_MAX, 0].
+__device__ __forceinline__ float minp_edge(float min_p) {
+    if (!(min_p <= 1.0f)) return INFINITY;
+    float x = (float)log((double)min_p);
+    for (int it = 0; it < 4 && !(exp_cr(x) >= min_p); ++it) x = nextafterf(x, INFINITY);
+    for (int it = 0; it < 4 && exp_cr(nextafterf(x, -INFINITY)) >= min_p; ++it) x = nextafterf(x, -INFINITY);
+    if (exp_cr(x) >= min_p && !(exp_cr(nextafterf(x, -INFINITY)) >= min_p)) return x;
+    int lo = f2ord(-__FLT_MAX__), hi = f2ord(0.0f);  // exp_cr(0) = 1 >= min_p
+    while (hi - lo > 1) {
+        const int mid = lo + (hi - lo) / 2;
+        if (exp_cr(ord2f(mid)) >= min_p) hi = mid;
+        else lo = mid;
+    }
+    return ord2f(hi);
+}
 
 // home slot of id t: the murmur3 finalizer, so that arithmetic progressions
 // of ids (a permuted vocabulary's top ranks, for one) do not cluster
@@ -1878,6 +1913,8 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     }
     if (tid == 0) {
         SL.next = 2u * NW;
+        SL.ncand = 0;
+        SL.ncap = 0;
         SL.err = 0;
         SL.bpos = 0;
         SL.gmax = f2ord(-INFINITY);
@@ -2037,18 +2074,23 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         }
         rthr = !fastp ? -INFINITY : (gather ? fminf(lpre, mrun) : mrun);
     };
-    // The wave's min-p candidates: slots by ballot (every lane of the wave
-    // calls these; wcand is the wave's running count)
-    Cand* candw = SL.cand[wv];
-    uint32_t wcand = 0;
+    // tot slots of a pool for the wave: one LDS atomic by lane 0 (every lane
+    // of the wave calls it)
+    auto claim = [&](uint32_t* ctr, uint32_t tot) -> uint32_t {
+        uint32_t b = 0;
+        if (lane == 0) b = atomicAdd(ctr, tot);
+        return (uint32_t)__builtin_amdgcn_readfirstlane((int)b);
+    };
+    // The row's min-p candidates: a run of pool slots per call, lanes placed
+    // by ballot (every lane of the wave calls these)
     auto append_one = [&](bool c, uint32_t e, float l) {
         const uint64_t m1 = __ballot(c);
-        const uint32_t pos = wcand + mbcnt64(m1);
-        if (c && pos < CANDW) {
-            candw[pos].id = e;
-            candw[pos].l = l;
+        if (m1 == 0ull) return;
+        const uint32_t pos = claim(&SL.ncand, (uint32_t)__popcll(m1)) + mbcnt64(m1);
+        if (c && pos < CANDP) {
+            SL.cand[pos].id = e;
+            SL.cand[pos].l = l;
         }
-        wcand += (uint32_t)__popcll(m1);
     };
     auto gsum_add = [&](float l) {
         if (isfinite(l)) {
@@ -2097,23 +2139,20 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         }
     };
     // The wave's lanes holding special elements (bits sk) append (id, raw
-    // value) to the wave's capture region; wcnt is the wave's running count.
-    Cand* capw = SL.cap[wv];
-    uint32_t wcnt = 0;
+    // value) to the capture pool.
     auto capture = [&](const u32x4& raw, uint32_t mw, uint32_t e0, uint32_t sk) {
         const uint64_t m1 = __ballot(sk != 0u);
         if (m1 == 0ull) return;
         const uint64_t m2 = __ballot((sk & (sk - 1u)) != 0u);
         if (m2 == 0ull) {
             // at most one special element per lane (the common case)
-            const uint32_t pos = wcnt + mbcnt64(m1);
-            if (sk != 0u && pos < CAPW) {
+            const uint32_t pos = claim(&SL.ncap, (uint32_t)__popcll(m1)) + mbcnt64(m1);
+            if (sk != 0u && pos < CAPP) {
                 const uint32_t q = (uint32_t)__ffs((int)sk) - 1u;
                 const bool off = MASK && !((mw >> ((e0 + q) & 31u)) & 1u);
-                capw[pos].id = (e0 + q) | (off ? CAP_OFF : 0u);
-                capw[pos].l = elem(raw, q);
+                SL.cap[pos].id = (e0 + q) | (off ? CAP_OFF : 0u);
+                SL.cap[pos].l = elem(raw, q);
             }
-            wcnt += (uint32_t)__popcll(m1);
         } else {
             // per-lane counts up to EPV: prefix from their bit slices
             const uint32_t c = (uint32_t)__popc(sk);
@@ -2124,18 +2163,17 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                 pre += mbcnt64(mb) << b;
                 tot += (uint32_t)__popcll(mb) << b;
             }
-            uint32_t pos = wcnt + pre;
+            uint32_t pos = claim(&SL.ncap, tot) + pre;
 #pragma unroll
             for (int q = 0; q < EPV; ++q)
                 if ((sk >> q) & 1u) {
-                    if (pos < CAPW) {
+                    if (pos < CAPP) {
                         const bool off = MASK && !((mw >> ((e0 + q) & 31u)) & 1u);
-                        capw[pos].id = (e0 + q) | (off ? CAP_OFF : 0u);
-                        capw[pos].l = unpack<DT>(raw, q);
+                        SL.cap[pos].id = (e0 + q) | (off ? CAP_OFF : 0u);
+                        SL.cap[pos].l = unpack<DT>(raw, q);
                     }
                     ++pos;
                 }
-            wcnt += tot;
         }
     };
     // Per vector: its maximum decides everything.  The thread keeps the
@@ -2180,13 +2218,12 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         if (m1 == 0ull) return;
         const uint64_t m2 = __ballot((qm & (qm - 1u)) != 0u);
         if (m2 == 0ull) {
-            const uint32_t pos = wcand + mbcnt64(m1);
-            if (qm != 0u && pos < CANDW) {
+            const uint32_t pos = claim(&SL.ncand, (uint32_t)__popcll(m1)) + mbcnt64(m1);
+            if (qm != 0u && pos < CANDP) {
                 const uint32_t q = (uint32_t)__ffs((int)qm) - 1u;
-                candw[pos].id = e0 + q;
-                candw[pos].l = elem(raw, q);
+                SL.cand[pos].id = e0 + q;
+                SL.cand[pos].l = elem(raw, q);
             }
-            wcand += (uint32_t)__popcll(m1);
         } else {
             const uint32_t c = (uint32_t)__popc(qm);
             uint32_t pre = 0, tot = 0;
@@ -2196,21 +2233,43 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                 pre += mbcnt64(mb) << b;
                 tot += (uint32_t)__popcll(mb) << b;
             }
-            uint32_t pos = wcand + pre;
+            uint32_t pos = claim(&SL.ncand, tot) + pre;
 #pragma unroll
             for (int q = 0; q < EPV; ++q)
                 if ((qm >> q) & 1u) {
-                    if (pos < CANDW) {
-                        candw[pos].id = e0 + q;
-                        candw[pos].l = unpack<DT>(raw, q);
+                    if (pos < CANDP) {
+                        SL.cand[pos].id = e0 + q;
+                        SL.cand[pos].l = unpack<DT>(raw, q);
                     }
                     ++pos;
                 }
-            wcand += tot;
         }
     };
+    // With the skip (fastp), a wave queues its relevant vectors in LDS
+    // (ballot slots) and looks at them 64 at a time, one lane per vector: a
+    // relevant vector is rare, and a look costs the whole wave.
+    uint32_t wq = 0;  // queued vectors (wave-uniform)
+    auto flush = [&]() {
+        if (wq == 0u) return;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const bool v = (uint32_t)lane < wq;
+        const u32x4 raw = v ? SL.qraw[wv][lane] : u32x4{0u, 0u, 0u, 0u};
+        const uint32_t e0 = v ? SL.qe0[wv][lane] : 0u;
+        const uint32_t mw = (MASK && v) ? SL.qmw[wv][lane] : 0xFFFFFFFFu;
+        const uint32_t sk = v ? spec_bits(e0) : 0u;
+        if (special) capture(raw, mw, e0, sk);
+        uint32_t qm = 0;
+        if (v) qm = look(raw, mw, e0, sk);
+        if (gather) append(raw, e0, qm);
+        wq = 0;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");  // read before the queue is refilled
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
     // Per vector: its raw maximum (special and disallowed elements included)
-    // against rthr; the wave looks closer only when some lane reaches it.
+    // against rthr; only vectors that reach it are looked at closer.
     auto process = [&](Tile<DT, TV, MASK>& T, uint32_t ch) {
         const uint32_t t0 = chunk_t0(ch), sl = chunk_slot(ch);
 #pragma unroll
@@ -2224,13 +2283,26 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             for (int q = 1; q < EPV; ++q) vr = fmaxf(vr, unpack<DT>(T.raw[j], q));
             // (an all-NaN vector is looked at: masked or banned, NaN is -inf)
             const bool rel = in && !(vr < rthr);
-            if (__ballot(rel) != 0ull) {
-                // whole wave: the capture keeps a wave-uniform count
-                const uint32_t sk = rel ? spec_bits(e0) : 0u;
-                if (special) capture(T.raw[j], mw, e0, sk);
-                uint32_t qm = 0;
-                if (rel) qm = look(T.raw[j], mw, e0, sk);
-                if (gather) append(T.raw[j], e0, qm);
+            const uint64_t bal = __ballot(rel);
+            if (bal != 0ull) {
+                if (fastp) {
+                    const uint32_t cnt = (uint32_t)__popcll(bal);
+                    if (wq + cnt > QN) flush();
+                    if (rel) {
+                        const uint32_t pos = wq + mbcnt64(bal);
+                        SL.qraw[wv][pos] = T.raw[j];
+                        SL.qe0[wv][pos] = e0;
+                        if (MASK) SL.qmw[wv][pos] = mw;
+                    }
+                    wq += cnt;
+                } else {
+                    // every vector is relevant: looked at in place (whole wave)
+                    const uint32_t sk = rel ? spec_bits(e0) : 0u;
+                    if (special) capture(T.raw[j], mw, e0, sk);
+                    uint32_t qm = 0;
+                    if (rel) qm = look(T.raw[j], mw, e0, sk);
+                    if (gather) append(T.raw[j], e0, qm);
+                }
             }
             __builtin_amdgcn_sched_barrier(0);
         }
@@ -2285,10 +2357,14 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     if (special && wv < HWAVES) build_hash();
     // the decision's per-row constants, off its critical path
     double lnmin = 0.0;
-    float urow = 0.0f;
+    float urow = 0.0f, xstar = INFINITY;
     if (gather && wv == 0) {
         lnmin = log((double)c.p.min_p);
+        xstar = minp_edge(c.p.min_p);
         urow = row_uniform(a, r, c.p);
+        // computed here, while the first tiles load: the compiler would
+        // otherwise sink them to their use after the stream
+        asm volatile("" : "+v"(lnmin), "+v"(xstar), "+v"(urow));
     }
     // Both buffers are refilled unconditionally (a claim past the end loads a
     // dummy line), so the wait for one buffer leaves the other's loads in
@@ -2298,6 +2374,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         if (c1 >= nchunk) break;
         step(b1, c1);
     }
+    flush();
     // the first element of the best vector that attains the maximum
     if (tj != NONE) {
         float v[EPV];
@@ -2308,22 +2385,23 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             if (v[q] == tm) q0 = (uint32_t)q;
         ta = tj + q0;
     }
-    if (special && lane == 0 && wcnt > CAPW) atomicOr(&SL.err, RERR_CAP);
     lds_barrier();
     // the special ids' processed values
     if (special) {
         auto cand_ok = [&](float l) {
             return gather && l > -INFINITY && (mrun == -INFINITY || __fmul_rn(__fsub_rn(l, mrun), inv) >= thr);
         };
-        if (!(SL.err & (RERR_HASH | RERR_CAP))) {
-            // each wave its own captures (whole-wave loop: the appends ballot)
-            for (uint32_t base = 0; base < wcnt; base += 64u) {
+        const uint32_t ncap = SL.ncap;
+        if (ncap <= CAPP && !(SL.err & RERR_HASH)) {
+            // the captures, 64 per wave at a time (whole-wave loop: the
+            // appends ballot)
+            for (uint32_t base = (uint32_t)wv * 64u; base < ncap; base += RT) {
                 const uint32_t i = base + (uint32_t)lane;
-                const bool ok = i < wcnt;
+                const bool ok = i < ncap;
                 uint32_t e = 0;
                 float l = NAN;
                 if (ok) {
-                    const Cand cd = capw[i];
+                    const Cand cd = SL.cap[i];
                     e = cd.id & ~CAP_OFF;
                     const uint32_t s = hash_find(SL.u.p.hkey, e);
                     const uint32_t hv = s == NONE ? 0u : SL.u.p.hval[s];
@@ -2334,12 +2412,10 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                 }
                 if (gather) append_one(ok && cand_ok(l), e, l);
             }
-            if (lane == 0) SL.wcn[wv] = wcand;
         } else {
-            // a full hash or capture region: every special id resolved from
-            // HBM (raw logit; window count and ban from the hash, or, when it
-            // is full, by scanning the history); candidates by LDS atomics
-            if (lane == 0) SL.wcn[wv] = wcand;
+            // a full hash or capture pool: every special id resolved from HBM
+            // (raw logit; window count and ban from the hash, or, when it is
+            // full, by scanning the history); candidates by LDS atomics
             const bool hok = !(SL.err & RERR_HASH);
             const uint32_t nw = (hi + 31u) / 32u;
             for (uint32_t wi = tid; wi < nw; wi += RT) {
@@ -2367,17 +2443,15 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                     am_merge(tm, ta, l, isnan(l) ? NONE : e);
                     if (gsum_on) gsum_add(l);
                     if (cand_ok(l)) {
-                        const uint32_t slot = atomicAdd(&SL.wcn[wv], 1u);
-                        if (slot < CANDW) {
-                            candw[slot].id = e;
-                            candw[slot].l = l;
+                        const uint32_t slot = atomicAdd(&SL.ncand, 1u);
+                        if (slot < CANDP) {
+                            SL.cand[slot].id = e;
+                            SL.cand[slot].l = l;
                         }
                     }
                 }
             }
         }
-    } else if (lane == 0) {
-        SL.wcn[wv] = wcand;
     }
 
     // row results: per-wave DPP reductions, merged by every thread
@@ -2397,10 +2471,10 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         SL.gs[wv] = wgs;
     }
     lds_barrier();
-    float m = SL.wm[0];
-    uint32_t am = SL.wa[0];
-#pragma unroll
-    for (int k = 1; k < RWV; ++k) am_merge(m, am, SL.wm[k], SL.wa[k]);
+    // the 16 results, one per lane, merged by DPP (every thread)
+    float m = lane < RWV ? SL.wm[lane] : -INFINITY;
+    uint32_t am = lane < RWV ? SL.wa[lane] : NONE;
+    wave_argmax_dpp(m, am);
     if (am == NONE) m = -INFINITY;
     double gsum = 0.0;
     if (gsum_on && isfinite(m)) {
@@ -2409,31 +2483,14 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             if (isfinite(SL.gm[k])) gsum += (double)SL.gs[k] * exp((double)SL.gm[k] - (double)m);
     }
     uint32_t flags = sflags;
-    uint32_t n = 0;
-    uint32_t pre[RWV];  // candidates before each wave's region
-#pragma unroll
-    for (int k = 0; k < RWV; ++k) {
-        pre[k] = n;
-        const uint32_t cw = gather ? SL.wcn[k] : 0u;
-        if (cw > CANDW) flags |= CS_OVERFLOW;
-        n += cw < CANDW ? cw : CANDW;
-    }
-    // the k-th candidate across the wave regions (unrolled selects: no
-    // dynamic indexing of registers)
-    auto cand_at = [&](uint32_t k) -> Cand {
-        uint32_t w = 0, base = 0;
-#pragma unroll
-        for (int q = 1; q < RWV; ++q)
-            if (k >= pre[q]) {
-                w = (uint32_t)q;
-                base = pre[q];
-            }
-        return (&SL.cand[0][0])[w * CANDW + (k - base)];
-    };
+    const uint32_t nc = gather ? SL.ncand : 0u;
+    if (nc > CANDP) flags |= CS_OVERFLOW;
+    const uint32_t n = nc < CANDP ? nc : CANDP;
+    auto cand_at = [&](uint32_t k) -> Cand { return SL.cand[k]; };
     if (gather && !(flags & (CS_ERROR | CS_OVERFLOW)) && am != NONE && isfinite(m) && n <= 256u) {
         // min-p row with few candidates: wave 0 decides alone
         if (wv != 0) return;
-        wave_decide_minp<RT>(a, r, c.p, m, inv, am, n, cand_at, (uint64_t*)SL.stage, SL.u.F, lnmin, urow);
+        wave_decide_minp<RT>(a, r, c.p, m, inv, am, n, cand_at, (uint64_t*)SL.stage, SL.u.F, lnmin, xstar, urow);
         return;
     }
     RowState xs;
