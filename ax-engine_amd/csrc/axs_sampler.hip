@@ -3442,9 +3442,11 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
     // (AXS_STREAM_WGS, default 1024: four per CU), segments a multiple of
     // MIN_CHUNK ids and at most SEG_MAX
     static const int target = env_int("AXS_STREAM_WGS", 1024);
-    // enough rows to give every CU one: each row is one 1024-thread workgroup
-    // that decides it in place (AXS_STREAM_WIDE_ROWS, default 240 rows)
-    static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 240);
+    // from 64 rows on, each row is one 1024-thread workgroup that decides it
+    // in place (AXS_STREAM_WIDE_ROWS): with fewer rows than CUs, each row's
+    // CU draws more than its 1/256 share of HBM bandwidth, and this beats
+    // the segmented shape's cross-workgroup merge (C2, 64 rows: 23 vs 46 us)
+    static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 64);
     pl.tv = 4;
     if (nrows >= wide_rows && (uint32_t)vocab <= ROW_MAX) {
         pl.wide = true;

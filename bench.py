@@ -253,7 +253,8 @@ def main():
     res = step(0)
     torch.cuda.synchronize()
     # the dominant kernel and its algorithmic bytes per launch
-    name0 = "k_row" if (cfg != "C5" and rows_per_step >= 240) else "k_stream"
+    pipeline_rows = rows_per_step * 7 if cfg == "C5" else rows_per_step  # C5: 4 target + 3 draft rows each
+    name0 = "k_row" if pipeline_rows >= 64 else "k_stream"
     kern = {(name0 if k == "k_stream" else k): v for k, v in kern.items()}
     dom = max(kern.items(), key=lambda kv: kv[1]["avg_us"])
     dom_name, dom_us = dom[0], dom[1]["avg_us"]

@@ -14,7 +14,7 @@ import pytest
 from ax_sampler import MlxSamplingParams, pack_params
 from ax_sampler import _abi
 from ax_sampler.synth import (DTYPE_BF16, DTYPE_F32, Workload, f32_to_bf16_bits, make_c1, make_c2,
-                              make_c3, make_c4)
+                              make_c3, make_c4, make_mixed)
 
 from gpu_common import compare, log, run_gpu, run_oracle
 
@@ -116,3 +116,14 @@ def test_c4_constrained(sampler, oracle):
     allowed = w.extra["allowed"]
     tid = gpu[0]
     assert all(allowed[r, tid[r]] for r in range(w.B)), "a masked id was emitted"
+
+
+@pytest.mark.parametrize("dtype,V", [(DTYPE_BF16, 151936), (DTYPE_F32, 4099)])
+def test_mixed_laws_segmented(sampler, oracle, dtype, V):
+    """Every row law, masks, bias lists and bans on the segmented shape
+    (fewer than 64 rows: k_stream, then k_exact_mat / k_exact_row)."""
+    w = make_mixed(21 + V % 89, 40, V, dtype, hist_len=512, mask=True, bias=True, ngram=True)
+    us = _uniforms(w.B, 2000 + V)
+    gpu = run_gpu(sampler, w, us, kept_cap=32)
+    cpu = run_oracle(oracle, w, us, kept_cap=32)
+    log(f"mixed segmented dtype={dtype} V={V}: {compare(w, gpu, cpu, f'mixed-seg-{V}')}")

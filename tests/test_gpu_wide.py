@@ -1,4 +1,4 @@
-"""GPU parity of the one-workgroup-per-row shape (k_row: batches of >= 240
+"""GPU parity of the one-workgroup-per-row shape (k_row: batches of >= 64
 rows, V <= 262,144) against the CPU oracle, through the C ABI.
 
 Same bar as test_gpu_parity: token ids bit-exact on every row the oracle does
