@@ -2343,17 +2343,6 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         load(T, ch);
         if (bound) raise(wave_max_dpp(tm));
     };
-    if (false) {
-        // every wave's first chunk seeds the bound with the block maximum
-        const float tmx = wave_max_dpp(c0 < nchunk ? tile_max(b0, c0) : -INFINITY);
-        if (lane == 0) SL.wm[wv] = tmx;
-        lds_barrier();
-        float mm = SL.wm[0];
-#pragma unroll
-        for (int k = 1; k < RWV; ++k) mm = fmaxf(mm, SL.wm[k]);
-        mrun = mm;
-        set_pre();
-    }
     if (special && wv < HWAVES) build_hash();
     // the decision's per-row constants, off its critical path
     double lnmin = 0.0;
