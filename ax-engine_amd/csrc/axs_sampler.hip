@@ -1,8 +1,15 @@
 // axs_sampler.hip — MI355X (gfx950) per-step token sampler behind the C ABI
 // of include/ax_hip_sampler.h.
 //
-// One sampling step over [rows, V] logits in HBM runs as three kernels on the
-// caller's stream:
+// One sampling step over [rows, V] logits in HBM runs on the caller's stream
+// as one kernel for batches of 64 rows or more:
+//
+//   k_row       one 1024-thread workgroup per row: the single pass over the
+//               logits (the HBM-bound kernel), the row's decision, and, for a
+//               row that needs it, the exact path (second read, sort, exact
+//               running sums, decisions) in the same workgroup;
+//
+// and as three kernels for smaller batches:
 //
 //   k_stream    the single pass over the logits (the HBM-bound kernel).  Work
 //               item = (row, segment of <= 65536 ids); the segments of a row
@@ -1684,14 +1691,16 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
 //   spec  a bit per id: in the window, biased or banned
 //   hkey/hval  an open-addressing hash of the special ids: window count,
 //         bias entry, n-gram ban
-// The stream reads special elements as NaN (never a maximum, never a
-// candidate) and captures their raw values from its registers into the
-// wave's LDS region (a ballot gives each lane its slot: no atomics); after
-// the stream each captured element gets every processor from the hash and
-// joins the maximum and the candidates.  No scattered loads.  The row's
-// maximum is merged from per-wave DPP reductions, and a min-p row with at
-// most 256 candidates is decided by wave 0 alone (register bitonic sort, no
-// block barriers).
+// A vector whose raw maximum reaches the running bound is rare; a wave queues
+// such vectors in LDS and looks at them 64 at a time, one lane each.  The look
+// reads special elements as NaN (never a maximum, never a candidate) and
+// captures their raw values into a shared capture pool (a wave claims a run
+// of slots with one LDS atomic, a ballot places its lanes); after the stream
+// each captured element gets every processor from the hash and joins the
+// maximum and the candidates.  No scattered loads.  The row's maximum is
+// merged from per-wave DPP reductions, and a min-p row with at most 256
+// candidates is decided by wave 0 alone (survivors by a precomputed exp edge,
+// ranked by LDS broadcasts, no block barriers).
 // --------------------------------------------------------------------------
 constexpr int RT = 1024;               // threads of a row workgroup
 constexpr int RWV = RT / 64;           // its waves
