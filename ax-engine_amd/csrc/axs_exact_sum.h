@@ -68,8 +68,10 @@ AXS_HD Binade binade_of(float s) {
     return r;
 }
 
-// s = A * 2^E, exact for A < 2^24.
+// s = A * 2^E, exact for A < 2^24: inside a normal binade (A >= 2^23) or in
+// the lowest one (E = -149) it is the bit pattern ((E + 149) << 23) + A.
 AXS_HD float binade_value(uint32_t A, int32_t E) {
+    if (E == -149 || A >= 0x00800000u) return bits_f32(((uint32_t)(E + 149) << 23) + A);
     return (float)ldexp((double)A, E);
 }
 
@@ -81,18 +83,28 @@ struct Term {
 };
 
 AXS_HD Term term_of(float x, int32_t E) {
-    double q = ldexp((double)x, -E);  // exact: a 24-bit value scaled by 2^-E
+    // x = M * 2^e2 with M its 24-bit significand; q = x / 2^E = M * 2^(e2 - E),
+    // split into integer part n and remainder r of sh bits, all in integers
+    const uint32_t b = f32_bits(x);
+    const uint32_t be = b >> 23;  // x >= 0: no sign bit
+    const uint32_t M = be ? ((b & 0x007FFFFFu) | 0x00800000u) : (b & 0x007FFFFFu);
+    const int32_t s = (be ? (int32_t)be - 150 : -149) - E;
     Term t;
-    if (q >= 33554432.0) {  // 2^25
-        t.c0 = t.c1 = 33554432u;
+    if (s >= 0) {
+        const uint64_t q = (uint64_t)M << (s < 40 ? s : 40);
+        t.c0 = t.c1 = q >= 33554432ull ? 33554432u : (uint32_t)q;  // saturated at 2^25
         return t;
     }
-    double n = floor(q);
-    double f = q - n;
-    uint32_t ni = (uint32_t)n;
-    if (f > 0.5) {
+    const uint32_t sh = (uint32_t)(-s);
+    if (sh >= 26u) {  // q < 2^24 / 2^26: rounds to 0
+        t.c0 = t.c1 = 0u;
+        return t;
+    }
+    const uint32_t ni = M >> sh;
+    const uint32_t r = M & ((1u << sh) - 1u), half = 1u << (sh - 1u);
+    if (r > half) {
         t.c0 = t.c1 = ni + 1u;
-    } else if (f < 0.5) {
+    } else if (r < half) {
         t.c0 = t.c1 = ni;
     } else {  // exact tie: round half to even on (s/U + n + 1/2)
         t.c0 = ni + (ni & 1u);

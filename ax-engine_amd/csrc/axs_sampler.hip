@@ -2702,11 +2702,11 @@ __device__ __forceinline__ Xd block_excl_scan_xd(Xd x, Xd* s_w) {
     if (lane == 63) s_w[w] = inc;
     Xd ex = shfl_up_xd(inc, 1);
     if (lane == 0) ex = xd_identity();
-    __syncthreads();
+    lds_barrier();  // LDS only: the caller's global loads and stores stay in flight
     Xd wp = xd_identity();
     for (int k = 0; k < NW; ++k)
         if (k < w) wp = xd_compose(wp, s_w[k]);
-    __syncthreads();
+    lds_barrier();
     return xd_compose(wp, ex);
 }
 
@@ -2874,6 +2874,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     // current sum; the first term that would leave it (the earliest crossing
     // over the block) is added directly by its thread, which sets the next
     // round's start.  The round's state stays in LDS.
+    // The round's barriers are LDS-only: S is read only after the loop.
     constexpr uint32_t IT = XI;
     if (tid == 0) s_cross = NONE;
     while (true) {
@@ -2917,8 +2918,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             S[i] = last;
         }
         if (mycross != NONE) atomicMin(&s_cross, mycross);
-        __threadfence_block();
-        __syncthreads();
+        lds_barrier();
         const uint32_t kc = s_cross;
         if (kc == NONE) {
             if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last term
@@ -2930,10 +2930,11 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             s_s = xs;
             s_k = kc + 1u;
         }
-        __threadfence_block();
-        __syncthreads();
+        lds_barrier();
         if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
     }
+    __threadfence_block();
+    __syncthreads();  // every S store complete before the decisions read S
 
     // index-order rows: the kept-set size and the ordered kept lists, by the
     // whole block
