@@ -2689,23 +2689,61 @@ __device__ __forceinline__ Xd shfl_up_xd(Xd x, int d) {
     return y;
 }
 
+// One DPP move of a transducer record (every dword); lanes without a source
+// (outside the row, or rows the mask leaves out) get the identity.
+template <int CTRL, int ROWS>
+__device__ __forceinline__ Xd dpp_xd(const Xd& x) {
+    auto mv = [](uint32_t old, uint32_t v) {
+        return (uint32_t)__builtin_amdgcn_update_dpp((int)old, (int)v, CTRL, ROWS, 0xF, false);
+    };
+    Xd y;
+    y.inc0 = ((uint64_t)mv(0u, (uint32_t)(x.inc0 >> 32)) << 32) | mv(0u, (uint32_t)x.inc0);
+    y.inc1 = ((uint64_t)mv(0u, (uint32_t)(x.inc1 >> 32)) << 32) | mv(0u, (uint32_t)x.inc1);
+    y.par0 = mv(0u, x.par0);
+    y.par1 = mv(1u, x.par1);
+    return y;
+}
+
+// Inclusive scan of transducer records over each 16-lane row (Hillis-Steele:
+// row shifts 1, 2, 4, 8; composition is associative, not commutative, and
+// the earlier lane's record goes first).
+__device__ __forceinline__ Xd row_incl_scan_xd(Xd x) {
+    x = xd_compose(dpp_xd<0x111, 0xF>(x), x);  // row_shr:1
+    x = xd_compose(dpp_xd<0x112, 0xF>(x), x);  // row_shr:2
+    x = xd_compose(dpp_xd<0x114, 0xF>(x), x);  // row_shr:4
+    x = xd_compose(dpp_xd<0x118, 0xF>(x), x);  // row_shr:8
+    return x;
+}
+
+__device__ __forceinline__ Xd readlane_xd(const Xd& x, int l) {
+    Xd y;
+    y.inc0 = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x.inc0 >> 32), l) << 32) |
+             (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x.inc0, l);
+    y.inc1 = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(x.inc1 >> 32), l) << 32) |
+             (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)x.inc1, l);
+    y.par0 = (uint32_t)__builtin_amdgcn_readlane((int)x.par0, l);
+    y.par1 = (uint32_t)__builtin_amdgcn_readlane((int)x.par1, l);
+    return y;
+}
+
+// Exclusive scan of transducer records over the block: within each wave by
+// DPP (rows, then row_bcast:15 into rows 1 and 3, row_bcast:31 into rows 2
+// and 3), across the waves by one DPP row scan of their totals.  Every
+// thread of the block calls it; LDS-only barriers.
 template <int NT>
 __device__ __forceinline__ Xd block_excl_scan_xd(Xd x, Xd* s_w) {
     constexpr int NW = NT / 64;
-    int w = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    Xd inc = x;
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        Xd y = shfl_up_xd(inc, d);
-        if (lane >= d) inc = xd_compose(y, inc);
-    }
+    static_assert(NW <= 16, "wave totals are scanned in one row");
+    const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    Xd inc = row_incl_scan_xd(x);
+    inc = xd_compose(dpp_xd<0x142, 0xA>(inc), inc);  // row_bcast:15 into rows 1, 3
+    inc = xd_compose(dpp_xd<0x143, 0xC>(inc), inc);  // row_bcast:31 into rows 2, 3
     if (lane == 63) s_w[w] = inc;
     Xd ex = shfl_up_xd(inc, 1);
     if (lane == 0) ex = xd_identity();
     lds_barrier();  // LDS only: the caller's global loads and stores stay in flight
-    Xd wp = xd_identity();
-    for (int k = 0; k < NW; ++k)
-        if (k < w) wp = xd_compose(wp, s_w[k]);
+    const Xd wt = row_incl_scan_xd(lane < NW ? s_w[lane] : xd_identity());
+    const Xd wp = w > 0 ? readlane_xd(wt, w - 1) : xd_identity();
     lds_barrier();
     return xd_compose(wp, ex);
 }
