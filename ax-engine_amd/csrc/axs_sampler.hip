@@ -167,6 +167,7 @@ struct KArgs {
     int32_t mtp_batch;
     int32_t want_logprob;
     int32_t vec;          // rows are 16-byte aligned: vector loads
+    int32_t inplace;      // k_row: a row's exact path in its own workgroup (else listed)
     int64_t stride;
     const axs_sampling_params* params;
     const axs_sampling_params* params2;
@@ -2502,6 +2503,13 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         },
         &xs);
     if (!ex) return;
+    if (!a.inplace) {  // listed for k_exact_mat / k_exact_row
+        if (tid == 0) {
+            a.rstate[r] = xs;
+            a.exact_rows[atomicAdd(a.exact_count, 1u)] = (uint32_t)r;
+        }
+        return;
+    }
 
     // The exact path in place (laws without min-p, candidate overflow): every
     // element's probability with the row maximum, from a second read of the
@@ -2597,7 +2605,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         xs.minp_mg = __float_as_uint(g);
     }
     xs.ncompact = SL.xn;
-    exact_row<4>(a, r, xs, SL.ex);
+    exact_row<8>(a, r, xs, SL.ex);
 }
 
 // --------------------------------------------------------------------------
@@ -3435,7 +3443,8 @@ struct Plan {
     uint32_t chunk;
     int nch;
     int tv;
-    bool wide;  // one 1024-thread workgroup per row
+    bool wide;     // one 1024-thread workgroup per row
+    bool inplace;  // ... which also takes the row's exact path
     uint32_t schunk;
     int snch;
     bool vec;
@@ -3479,14 +3488,21 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
     // (AXS_STREAM_WGS, default 1024: four per CU), segments a multiple of
     // MIN_CHUNK ids and at most SEG_MAX
     static const int target = env_int("AXS_STREAM_WGS", 1024);
-    // from 64 rows on, each row is one 1024-thread workgroup that decides it
-    // in place (AXS_STREAM_WIDE_ROWS): with fewer rows than CUs, each row's
-    // CU draws more than its 1/256 share of HBM bandwidth, and this beats
-    // the segmented shape's cross-workgroup merge (C2, 64 rows: 23 vs 46 us)
-    static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 64);
+    // From 2 rows on, each row is one 1024-thread workgroup that decides it in
+    // place (AXS_STREAM_WIDE_ROWS): with fewer rows than CUs, each row's CU
+    // draws more than its 1/256 share of HBM bandwidth, and this beats the
+    // segmented shape's cross-workgroup merge (min-p rows, 8 to 64 of them:
+    // 2-4x).  A row that needs the exact second pass takes it in its own
+    // workgroup from 64 rows on (AXS_INPLACE_ROWS: no further launch); below,
+    // it is listed for k_exact_mat, which spreads the pass over the idle CUs
+    // (a row's every probability needs a correctly rounded exp).
+    static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 2);
+    static const int inplace_rows = env_int("AXS_INPLACE_ROWS", 64);
     pl.tv = 4;
+    pl.inplace = false;
     if (nrows >= wide_rows && (uint32_t)vocab <= ROW_MAX) {
         pl.wide = true;
+        pl.inplace = nrows >= inplace_rows;
         pl.schunk = (uint32_t)vocab;
         pl.snch = 1;
         pl.vec = ((uintptr_t)base % 16 == 0) && ((stride * es) % 16 == 0) &&
@@ -3585,6 +3601,7 @@ int apply_plan(KArgs& a, const Plan& pl) {
     a.snch = pl.snch;
     a.schunk = (int32_t)pl.schunk;
     a.vec = pl.vec ? 1 : 0;
+    a.inplace = pl.inplace ? 1 : 0;
     return AXS_OK;
 }
 
@@ -3637,7 +3654,7 @@ int run_pipeline(axs_context* c, KArgs& a, const Plan& pl, hipStream_t s) {
     if (rc) return rc;
     fill_ws(a, c);
     timed(c, AXS_KERNEL_STREAM, s, [&] { launch_stream(pl, a, s); });
-    if (pl.wide) {  // k_row takes the exact path in place
+    if (pl.wide && pl.inplace) {  // k_row takes the exact path in place
         AXS_HIP_CHECK(hipGetLastError());
         return AXS_OK;
     }

@@ -120,8 +120,9 @@ def test_c4_constrained(sampler, oracle):
 
 @pytest.mark.parametrize("dtype,V", [(DTYPE_BF16, 151936), (DTYPE_F32, 4099)])
 def test_mixed_laws_segmented(sampler, oracle, dtype, V):
-    """Every row law, masks, bias lists and bans on the segmented shape
-    (fewer than 64 rows: k_stream, then k_exact_mat / k_exact_row)."""
+    """Every row law, masks, bias lists and bans on 40 rows: k_row, with the
+    rows that need the exact second pass listed for k_exact_mat /
+    k_exact_row."""
     w = make_mixed(21 + V % 89, 40, V, dtype, hist_len=512, mask=True, bias=True, ngram=True)
     us = _uniforms(w.B, 2000 + V)
     gpu = run_gpu(sampler, w, us, kept_cap=32)

@@ -1,5 +1,5 @@
-"""GPU parity of the one-workgroup-per-row shape (k_row: batches of >= 64
-rows, V <= 262,144) against the CPU oracle, through the C ABI.
+"""GPU parity of the one-workgroup-per-row shape (k_row: batches of 2 rows or
+more, V <= 262,144) against the CPU oracle, through the C ABI.
 
 Same bar as test_gpu_parity: token ids bit-exact on every row the oracle does
 not flag as a boundary row, kept sets exact, logprobs within 1e-5 relative.
@@ -109,8 +109,8 @@ def test_hash_overflow_fallback(sampler, oracle):
 @pytest.mark.parametrize("B", [256, 16])
 def test_min_p_above_one(sampler, oracle, B):
     """min_p > 1 leaves no survivor (the maximum has p = 1): argmax, no draw
-    (sampling.rs:290-293), for every draw law, on both the one-row-per-
-    workgroup shape (B = 256) and the segmented one (B = 16)."""
+    (sampling.rs:290-293), for every draw law, on the one-row-per-workgroup
+    shape (B = 256: exact path in place; B = 16: listed)."""
     w = make_c3(8, B=B, V=65536)
     rng = np.random.default_rng(88)
     w.params["min_p"] = rng.choice(np.array([1.5, 0.05, 2.0], np.float32), B)
