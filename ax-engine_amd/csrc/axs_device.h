@@ -367,67 +367,6 @@ __device__ __forceinline__ uint32_t pdesc_id(uint64_t k) { return ~(uint32_t)k; 
 __device__ __forceinline__ float idasc_p(uint64_t k) { return __uint_as_float((uint32_t)k); }
 __device__ __forceinline__ uint32_t idasc_id(uint64_t k) { return ~(uint32_t)(k >> 32); }
 
-__device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int m) {
-    uint32_t lo = (uint32_t)v, hi = (uint32_t)(v >> 32);
-    lo = (uint32_t)__shfl_xor((int)lo, m, 64);
-    hi = (uint32_t)__shfl_xor((int)hi, m, 64);
-    return ((uint64_t)hi << 32) | lo;
-}
-
-// Descending bitonic sort of one u64 per lane across a 64-lane wave.
-__device__ __forceinline__ uint64_t wave_sort_desc(uint64_t key) {
-    int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-        for (int j = k >> 1; j > 0; j >>= 1) {
-            uint64_t o = shfl_xor_u64(key, j);
-            bool desc = (lane & k) == 0;
-            bool lower = (lane & j) == 0;
-            uint64_t mx = key > o ? key : o;
-            uint64_t mn = key > o ? o : key;
-            key = (desc == lower) ? mx : mn;
-        }
-    }
-    return key;
-}
-
-// Descending bitonic sort of 256 u64 keys held four per lane by one wave:
-// element i = j * 64 + lane is k[j].
-__device__ __forceinline__ void wave_sort_desc4(uint64_t k[4]) {
-    const int lane = threadIdx.x & 63;
-#pragma unroll
-    for (int size = 2; size <= 256; size <<= 1) {
-#pragma unroll
-        for (int d = size >> 1; d > 0; d >>= 1) {
-            if (d >= 64) {
-                const int dj = d >> 6;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    if (j & dj) continue;  // each pair (j, j + dj) once
-                    const int j2 = j | dj;
-                    const bool desc = ((j * 64 + lane) & size) == 0;
-                    const uint64_t x = k[j], y = k[j2];
-                    const bool swap = desc ? (x < y) : (x > y);
-                    k[j] = swap ? y : x;
-                    k[j2] = swap ? x : y;
-                }
-            } else {
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const int i = j * 64 + lane;
-                    const uint64_t o = shfl_xor_u64(k[j], d);
-                    const bool desc = (i & size) == 0;
-                    const bool lower = (i & d) == 0;
-                    const uint64_t mx = k[j] > o ? k[j] : o;
-                    const uint64_t mn = k[j] > o ? o : k[j];
-                    k[j] = (desc == lower) ? mx : mn;
-                }
-            }
-        }
-    }
-}
-
 // Descending bitonic sort of n (a power of two) keys in memory `s` (LDS or
 // global) by the whole block.
 template <int NT>
