@@ -123,3 +123,26 @@ def test_min_p_above_one(sampler, oracle, B):
     big = w.params["min_p"] > 1.0
     assert np.array_equal(gpu[0][big], cpu[0][big])
     assert not np.any(gpu[2][big] & np.uint32(0x4)), "a row without survivors consumed a uniform"
+
+
+@pytest.mark.parametrize("B", [256, 16])
+def test_capture_pool_overflow(sampler, oracle, B):
+    """A repetition penalty below 1 can raise a logit, so every vector is
+    looked at and every special element captured; windows of 3,000 distinct
+    ids overflow the 2,048-entry capture pool (not the 4,096-slot hash), and
+    those rows resolve their special ids from HBM.  Same result as the
+    oracle."""
+    w = make_c3(9, B=B, V=65536)
+    rng = np.random.default_rng(99)
+    lens = np.full(w.B, 64, dtype=np.int64)
+    lens[: min(4, B)] = 3000
+    w.hist = np.concatenate([rng.permutation(w.V)[:n].astype(np.uint32) if n > 64 else
+                             rng.integers(0, w.V, n).astype(np.uint32) for n in lens])
+    w.hist_off = np.zeros(w.B + 1, dtype=np.int64)
+    w.hist_off[1:] = np.cumsum(lens)
+    w.params["repetition_penalty"] = np.where(np.arange(w.B) % 2 == 0, 0.9, 1.2).astype(np.float32)
+    w.params["repetition_context_size"] = 0xFFFFFFFF
+    us = _uniforms(w.B, 909)
+    gpu = run_gpu(sampler, w, us, kept_cap=16)
+    cpu = run_oracle(oracle, w, us, kept_cap=16)
+    log(f"capture pool overflow, B={B}: {compare(w, gpu, cpu, f'capture-overflow-{B}')}")
