@@ -3495,7 +3495,7 @@ Plan make_plan(int dtype, int nrows, int vocab, const void* base, int64_t stride
     // 2-4x).  A row that needs the exact second pass takes it in its own
     // workgroup from 64 rows on (AXS_INPLACE_ROWS: no further launch); below,
     // it is listed for k_exact_mat, which spreads the pass over the idle CUs
-    // (a row's every probability needs a correctly rounded exp).
+    // (one workgroup per row reading it again is slower: measured).
     static const int wide_rows = env_int("AXS_STREAM_WIDE_ROWS", 2);
     static const int inplace_rows = env_int("AXS_INPLACE_ROWS", 64);
     pl.tv = 4;
