@@ -1685,10 +1685,10 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
 
 // --------------------------------------------------------------------------
 // k_row: one 1024-thread workgroup per row (large batches), the row decided
-// in place.  The logits stream starts at once: waves HWAVES.. issue their
-// first two chunks' loads before anything else, while waves 0..HWAVES-1 fetch
-// the repetition window first (their loads would otherwise queue behind the
-// tiles) and stage it in LDS.  The special-id tables are then
+// in place.  The logits stream starts at once: every wave issues its first
+// chunk's loads, reads the row's context, issues its share of the repetition
+// window (which then queues behind one chunk per wave, not two) and then its
+// second chunk; the window is staged in LDS.  The special-id tables are then
 //   spec  a bit per id: in the window, biased or banned
 //   hkey/hval  an open-addressing hash of the special ids: window count,
 //         bias entry, n-gram ban
@@ -1902,25 +1902,21 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         }
     };
     uint32_t c0 = (uint32_t)wv, c1 = NW + (uint32_t)wv;
+    // Every wave: its first chunk, the row's context, its share of the
+    // window's first HPRE tokens, then its second chunk (the window's loads
+    // queue behind one chunk per wave, not two).
     Tile<DT, TV, MASK> b0, b1;
-    if (wv >= HWAVES) {
-        load(b0, c0);
-        load(b1, c1);
-    }
+    load(b0, c0);
     const RowCtx c = make_ctx(a, r);
     const bool special = c.cnt_on || c.bias_on || c.ban_on;
-    // the window's first HPRE tokens (waves 0..HWAVES-1, ahead of their tiles)
-    constexpr int HK = (int)(HPRE / (HWAVES * 64));
+    constexpr int HK = (int)(HPRE / RT);
     uint32_t ht[HK];
-    if (wv < HWAVES) {
 #pragma unroll
-        for (int k = 0; k < HK; ++k) {
-            const int64_t i = c.w0 + tid + (int64_t)k * (HWAVES * 64);
-            ht[k] = (c.cnt_on && i < c.w1) ? a.hist[i] : NONE;
-        }
-        load(b0, c0);
-        load(b1, c1);
+    for (int k = 0; k < HK; ++k) {
+        const int64_t i = c.w0 + tid + (int64_t)k * RT;
+        ht[k] = (c.cnt_on && i < c.w1) ? a.hist[i] : NONE;
     }
+    load(b1, c1);
     if (tid == 0) {
         SL.next = 2u * NW;
         SL.ncand = 0;
@@ -1964,10 +1960,8 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             }
             if (pos) SL.bpos = 1u;
         }
-        if (wv < HWAVES) {
 #pragma unroll
-            for (int k = 0; k < HK; ++k) SL.stage[tid + k * (HWAVES * 64)] = ht[k];
-        }
+        for (int k = 0; k < HK; ++k) SL.stage[tid + k * RT] = ht[k];
     }
     lds_barrier();
     // The bitmap, which the stream needs, is marked by every thread; the hash
