@@ -1,5 +1,5 @@
 // axs_device.h — device-side building blocks of the gfx950 sampler:
-// row-parameter decoding, Philox, exact exp, wave/block reductions and sorts.
+// row-parameter decoding, Philox, the reference's exp, wave/block reductions and sorts.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -7,6 +7,7 @@
 
 #include "../../include/ax_hip_sampler.h"
 #include "axs_exact_sum.h"
+#include "axs_expf.h"
 
 namespace axs {
 
@@ -91,18 +92,16 @@ __device__ __forceinline__ float philox_uniform(uint64_t seed, uint32_t row, uin
 }
 
 // ---------------------------------------------------------------------------
-// exp with a correctly rounded f32 result: the double exp (< 1 ulp in f64)
-// rounded once to f32.  glibc's expf, which the reference calls, is correctly
-// rounded for all but ~1e-4 of inputs (0.502 ulp); the two differ by one ulp
-// there, which only matters for rows flagged near a boundary.
+// exp as the reference computes it: f32::exp is the host libm's expf, which
+// axs_expf.h restates bit for bit (checked over all 2^32 inputs on the CPU).
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float exp_cr(float x) { return (float)exp((double)x); }
+__device__ __forceinline__ float exp_ref(float x) { return expf_libm(x); }
 
 // the reference's probability of a logit: exp((l - m) * inv), non-finite → 0
 // (sampling.rs:248-251, 274-277)
 __device__ __forceinline__ float prob_of(float l, float m, float inv) {
     float x = __fmul_rn(__fsub_rn(l, m), inv);
-    float p = exp_cr(x);
+    float p = exp_ref(x);
     return isfinite(p) ? p : 0.0f;
 }
 

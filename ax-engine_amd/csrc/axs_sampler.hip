@@ -36,7 +36,8 @@
 // Arithmetic follows sample_categorical_into
 // (crates/ax-engine-mlx/src/sampling.rs:204-316) operation by operation:
 // f32 round-to-nearest, no contraction (the file is built with
-// -ffp-contract=off), correctly rounded division.
+// -ffp-contract=off), correctly rounded division, and the host libm's expf
+// restated bit for bit (axs_expf.h).
 
 #include <hip/hip_runtime.h>
 
@@ -1075,8 +1076,8 @@ __device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_s
 // superset of its min-p survivors, sampling.rs:283-294): survivors p =
 // exp((l - m) / T) >= min_p, ordered by (p desc, id asc) — or by id for an
 // index-order draw — then decide_sorted.  x = (l - m) / T survives iff
-// x >= xstar, the smallest f32 whose correctly rounded exp reaches min_p (exp
-// is monotone), so only survivors need their exp: after the ballot
+// x >= xstar, the smallest f32 whose exp reaches min_p (the libm expf is
+// monotone on x <= 0, checked exhaustively), so only survivors need their exp: after the ballot
 // compaction into kbuf (LDS scratch of 256 keys, free once the candidates are
 // read) each lane computes its survivors' in parallel.  Candidates within
 // 1e-5 of ln(min_p) also get theirs, for the boundary flag.  The keys are then
@@ -1132,7 +1133,7 @@ __device__ __forceinline__ void wave_decide_minp(const KArgs& a, int r, const ax
         my[q] = 0ull;
         if (i < ns) {
             const uint64_t xk = kbuf[i];
-            const float pr = prob_of(__uint_as_float((uint32_t)(xk >> 32)), 0.0f, 1.0f);  // exp_cr(x): x - 0, * 1 exact
+            const float pr = prob_of(__uint_as_float((uint32_t)(xk >> 32)), 0.0f, 1.0f);  // exp_ref(x): x - 0, * 1 exact
             my[q] = sorted ? key_pdesc(pr, (uint32_t)xk) : key_idasc(pr, (uint32_t)xk);
         }
     }
@@ -1774,19 +1775,19 @@ __device__ __forceinline__ int f2ord(float f) {
 }
 __device__ __forceinline__ float ord2f(int k) { return __int_as_float(k >= 0 ? k : k ^ 0x7FFFFFFF); }
 
-// The smallest f32 x with exp_cr(x) >= min_p (+inf when none, min_p > 1):
+// The smallest f32 x with exp_ref(x) >= min_p (+inf when none, min_p > 1):
 // ln(min_p) rounded, moved by ulps; where exp rounds to the same value over
 // many ulps (near 0), a bisection over the ordered encoding of [-FLT_MAX, 0].
 __device__ __forceinline__ float minp_edge(float min_p) {
     if (!(min_p <= 1.0f)) return INFINITY;
     float x = (float)log((double)min_p);
-    for (int it = 0; it < 4 && !(exp_cr(x) >= min_p); ++it) x = nextafterf(x, INFINITY);
-    for (int it = 0; it < 4 && exp_cr(nextafterf(x, -INFINITY)) >= min_p; ++it) x = nextafterf(x, -INFINITY);
-    if (exp_cr(x) >= min_p && !(exp_cr(nextafterf(x, -INFINITY)) >= min_p)) return x;
-    int lo = f2ord(-__FLT_MAX__), hi = f2ord(0.0f);  // exp_cr(0) = 1 >= min_p
+    for (int it = 0; it < 4 && !(exp_ref(x) >= min_p); ++it) x = nextafterf(x, INFINITY);
+    for (int it = 0; it < 4 && exp_ref(nextafterf(x, -INFINITY)) >= min_p; ++it) x = nextafterf(x, -INFINITY);
+    if (exp_ref(x) >= min_p && !(exp_ref(nextafterf(x, -INFINITY)) >= min_p)) return x;
+    int lo = f2ord(-__FLT_MAX__), hi = f2ord(0.0f);  // exp_ref(0) = 1 >= min_p
     while (hi - lo > 1) {
         const int mid = lo + (hi - lo) / 2;
-        if (exp_cr(ord2f(mid)) >= min_p) hi = mid;
+        if (exp_ref(ord2f(mid)) >= min_p) hi = mid;
         else lo = mid;
     }
     return ord2f(hi);
@@ -3198,6 +3199,9 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         const float* tp_l = a.ws_kept_p + (size_t)tr * KEPT_CAP;
         const uint32_t* did_l = a.ws_kept_id + (size_t)dr * KEPT_CAP;
         const float* dp_l = a.ws_kept_p + (size_t)dr * KEPT_CAP;
+        // every wave has read the previous position's s_ft / s_fd (an accept
+        // continues straight here) before thread 0 clears them
+        __syncthreads();
         if (tid == 0) {
             s_ft = -1;
             s_fd = -1;
@@ -3216,12 +3220,13 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         float lps = lnq;
         if (Td > 0.0f && Tt > 0.0f && fabsf(__fsub_rn(Td, Tt)) > 1e-6f)
             lps = __fmul_rn(lnq, __fdiv_rn(Td, Tt));
-        float pdraft = fmaxf(exp_cr(lps), 1e-37f);
+        float pdraft = fmaxf(exp_ref(lps), 1e-37f);
         float accp = fminf(__fdiv_rn(pt, pdraft), 1.0f);
         float u = a.uniforms ? a.uniforms[(size_t)b * (D + 1) + i]
                              : philox_uniform(tp.seed, (uint32_t)b, tp.step, 1u + (uint32_t)i / 4u,
                                               (uint32_t)i & 3u);
-        if (fabs((double)u - (double)accp) < 1e-6) flags |= AXS_MTP_FLAG_NEAR_ACCEPT;
+        // u >= 1 never accepts, whatever accp <= 1 rounds to
+        if (u < 1.0f && fabs((double)u - (double)accp) < 1e-6) flags |= AXS_MTP_FLAG_NEAR_ACCEPT;
         if (u < accp) {
             if (tid == 0) out_ids[(size_t)b * (D + 1) + count] = d;
             ++count;

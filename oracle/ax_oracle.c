@@ -947,7 +947,8 @@ uint32_t axo_mtp_verify_seq(const float* target, const float* draft, uint32_t V,
         float p_draft = fmaxf(expf(lps), 1e-37f);
         float accept_prob = fminf(p_target / p_draft, 1.0f);
         float u = uniforms[i];
-        if (fabs((double)u - (double)accept_prob) < 1e-6) fl |= AXS_MTP_FLAG_NEAR_ACCEPT;
+        /* u >= 1 never accepts, whatever accept_prob <= 1 rounds to */
+        if (u < 1.0f && fabs((double)u - (double)accept_prob) < 1e-6) fl |= AXS_MTP_FLAG_NEAR_ACCEPT;
         if (u < accept_prob) {
             out_ids[count++] = d;
             ac++;

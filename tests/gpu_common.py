@@ -54,25 +54,33 @@ def run_oracle(oracle, w: Workload, uniforms=None, kept_cap=0, nthreads=8):
                                kept_cap=kept_cap, nthreads=nthreads)
 
 
+def boundary_allowance(rows: int, frac: float = 0.02) -> int:
+    """Most near-boundary MTP sequences a parity test excuses: 2% of them, at
+    least 1."""
+    return max(1, int(np.ceil(frac * rows)))
+
+
 def compare(w: Workload, gpu, cpu, name="", check_kept=True):
-    """Token ids must be equal on every row the oracle does not flag as a
-    boundary row; returns a summary dict."""
+    """Token ids must be equal on EVERY row, boundary rows included: the
+    device computes the reference's probabilities with the same libm expf
+    and reproduces its sequential f32 sums bit for bit, so a row near a
+    nucleus / min-p / draw boundary (which the oracle flags and the summary
+    counts) is decided identically on both sides.  Kept lists are compared
+    exactly on every row, logprobs within 1e-5 relative.  Returns a summary
+    dict."""
     tid, lp, fl, kid, kc = gpu
     want, ex, kept = cpu
     mism = np.nonzero(tid != want)[0]
     bnd = ex["boundary"] != 0
-    unexplained = [int(r) for r in mism if not bnd[r]]
-    assert not unexplained, (
-        f"{name}: token mismatch on non-boundary rows {unexplained[:10]}: "
-        f"gpu {tid[unexplained[:10]]} cpu {want[unexplained[:10]]} "
-        f"flags {[hex(int(f)) for f in fl[unexplained[:10]]]}"
+    assert mism.size == 0, (
+        f"{name}: token mismatch on rows {mism[:10].tolist()} (boundary: {bnd[mism[:10]].tolist()}): "
+        f"gpu {tid[mism[:10]]} cpu {want[mism[:10]]} "
+        f"flags {[hex(int(f)) for f in fl[mism[:10]]]}"
     )
     assert not np.any(fl & np.uint32(_abi.FLAG_ERROR)), f"{name}: error flag set"
     nk = 0
     if check_kept and kid is not None and kept is not None:
         for r in range(w.B):
-            if bnd[r]:
-                continue
             n = min(int(ex[r]["n_kept"]), kid.shape[1])
             assert int(kc[r]) == int(ex[r]["n_kept"]), (name, r, int(kc[r]), int(ex[r]["n_kept"]))
             # the exact path lists never-drawn entries (p < 2^-24 of the
@@ -87,7 +95,7 @@ def compare(w: Workload, gpu, cpu, name="", check_kept=True):
             nk += 1
     drew = ex["drew"] != 0
     if lp is not None:
-        sel = drew & ~bnd & (want == tid)
+        sel = drew
         if sel.any():
             np.testing.assert_allclose(lp[sel], ex["logprob"][sel], rtol=1e-5, atol=2e-6)
     return {

@@ -5,8 +5,11 @@ crates/ax-engine-mlx/src/sampling.rs:647-752).
 
 Per sequence the emitted ids (accepted prefix + residual / bonus tail), their
 count and the accept count must equal the oracle's, except on sequences the
-oracle flags as near a decision boundary (|u - p/q| < 1e-6, or a near flag in
-one of the sequence's distributions), which are counted.  Draft ids are drawn
+oracle flags as near a decision boundary (|u - p/q| < 1e-6 with u < 1, or a
+near flag in one of the sequence's distributions), which are counted and
+bounded (at most 2% of the sequences, at least 1).  u = 1 never accepts on
+either side, so the empty-residual fallback of draft == target is held
+exactly.  Draft ids are drawn
 from the draft law by the oracle with its own uniforms (config C5).
 """
 import numpy as np
@@ -15,7 +18,7 @@ import pytest
 from ax_sampler import _abi
 from ax_sampler.synth import DTYPE_BF16, DTYPE_F32, f32_to_bf16_bits, make_c5
 
-from gpu_common import log
+from gpu_common import boundary_allowance, log
 
 pytestmark = pytest.mark.gpu
 
@@ -63,6 +66,8 @@ def _run(sampler, oracle, tgt, dft, dtype, tp, dp, dids, us, name):
     c_ids, c_n, c_ac, c_fl = oracle.mtp_verify_batch(tgt, dft, dtype, B, D, V, V, dids, tp, dp,
                                                      uniforms=us, nthreads=8)
     near = (c_fl & np.uint32(NEAR)) != 0
+    assert int(near.sum()) <= boundary_allowance(B), (
+        f"{name}: {int(near.sum())} of {B} sequences near a boundary")
     bad = []
     for b in range(B):
         same = g_n[b] == c_n[b] and g_ac[b] == c_ac[b] and np.array_equal(g_ids[b, :g_n[b]],

@@ -1,8 +1,8 @@
 """GPU parity of the one-workgroup-per-row shape (k_row: batches of 2 rows or
 more, V <= 262,144) against the CPU oracle, through the C ABI.
 
-Same bar as test_gpu_parity: token ids bit-exact on every row the oracle does
-not flag as a boundary row, kept sets exact, logprobs within 1e-5 relative.
+Same bar as test_gpu_parity: token ids bit-exact on every row (boundary rows
+included, and counted), kept sets exact, logprobs within 1e-5 relative.
 Covers the north-star workload at full size (B=256, V=262,144 bf16) with
 supplied and Philox uniforms, every row law with masks, bias lists (duplicate
 and out-of-vocabulary ids) and n-gram bans, unaligned and tiny vocabularies,

@@ -272,3 +272,232 @@ def test_core_logprob_closed_form(oracle):
     l64 = logits.astype(np.float64)
     assert tok == int(np.argmax(logits))
     assert abs(lp - (-math.log(np.sum(np.exp(l64 - l64.max()))))) < 1e-5
+
+
+def _apply(oracle, row, mp, hist=(), mask=None, bias=None):
+    out = np.array(row, dtype=np.float32)
+    h = np.array(list(hist) if len(hist) else [0], dtype=np.uint32)
+    bi = bv = None
+    nb = 0
+    if bias is not None:
+        bi = np.array([b[0] for b in bias], dtype=np.uint32)
+        bv = np.array([b[1] for b in bias], dtype=np.float32)
+        nb = len(bias)
+    oracle.lib().axo_apply_processors(out.ctypes.data, out.size, P(mp).ctypes.data, h.ctypes.data,
+                                      len(hist), None if mask is None else mask.ctypes.data,
+                                      None if bi is None else bi.ctypes.data,
+                                      None if bv is None else bv.ctypes.data, nb)
+    return out
+
+
+def test_logit_bias_closed_form(oracle):
+    """Build extension: each bias entry is added to its id in list order (so
+    duplicates add one after another in f32), ids >= V are ignored, the bias
+    comes after repetition and presence / frequency, and the mask after the
+    bias.  The values are chosen so that every plausible other order gives a
+    different f32 result."""
+    f = np.float32
+    row = [1.0, 1.0, 3.0, 0.5, -1.0]
+    mp = MlxSamplingParams.greedy()
+    mp.repetition_penalty = 2.0
+    mp.presence_penalty, mp.frequency_penalty = 0.5, 0.25
+    hist = [2, 2, 1]
+    bias = [(0, 1e8), (0, -1e8), (0, 1.0),   # id 0: ((1 + 1e8) - 1e8) + 1 = 1 in f32
+            (7, 5.0),                         # id 7 >= V: ignored
+            (1, 1e-8),                        # id 1: after rep / presence: 1e-8
+            (2, -0.25), (3, 4.0)]
+    words = np.array([0b10111], dtype=np.uint32)  # id 3 disallowed
+    out = _apply(oracle, row, mp, hist, mask=words, bias=bias)
+    l0 = f(f(f(f(1.0) + f(1e8)) - f(1e8)) + f(1.0))
+    assert l0 == f(1.0)  # list order; summing the biases first would give 2, reversed 0
+    # id 1: history count 1 → rep 1/2 = 0.5, - 0.25 - 0.5 = -0.25 ... then + 1e-8
+    l1 = f(f(f(f(1.0) / f(2.0)) - f(0.25)) - f(0.5))
+    l1 = f(l1 + f(1e-8))
+    # id 2: count 2 → 3 / 2 = 1.5, - 0.5 - 0.5 = 0.5, + (-0.25) = 0.25
+    l2 = f(f(f(f(f(3.0) / f(2.0)) - f(f(0.25) * f(2.0))) - f(0.5)) + f(-0.25))
+    want = [l0, l1, l2, -np.inf, f(-1.0)]
+    assert out.tolist() == [float(w) for w in want], out
+    # rep before presence: presence first would give (3 - 0.5 - 0.5) / 2 = 1.0
+    assert l2 == f(0.25)
+    # bias after presence / frequency: adding 1e-8 to 1.0 first would be lost
+    assert l1 == f(-0.25) + f(1e-8) and l1 != f(-0.25)
+
+
+def test_logit_bias_decides_the_draw(oracle):
+    """A bias large enough to make an id the maximum makes it the greedy
+    token and the only survivor of top_k = 1; an out-of-vocabulary bias id
+    changes nothing."""
+    rs = np.random.default_rng(12)
+    V = 300
+    logits = rs.normal(0, 2, V).astype(np.float32)
+    t = int(np.argmin(logits))
+    bias_ids = np.array([t, V + 3], dtype=np.uint32)
+    bias_vals = np.array([100.0, 1e9], dtype=np.float32)
+    for mp in (MlxSamplingParams.greedy(), MlxSamplingParams.new(0.8, 1.0, 1)):
+        tok, _, _ = oracle.sample_row(logits, P(mp), [], u=0.5, bias_ids=bias_ids, bias_vals=bias_vals)
+        assert tok == t
+    tok, _, _ = oracle.sample_row(logits, P(MlxSamplingParams.greedy()), [], u=0.5,
+                                  bias_ids=bias_ids[1:], bias_vals=bias_vals[1:])
+    assert tok == int(np.argmax(logits))
+
+
+def test_full_vocab_token_logprob_closed_form(oracle):
+    """full_vocab_token_logprob (crates/ax-engine-mlx/src/sampling.rs:761-787)
+    against float64 log-softmax, plus its special cases."""
+    rs = np.random.default_rng(13)
+    V = 5000
+    logits = rs.normal(0, 3, V).astype(np.float32)
+    l64 = logits.astype(np.float64)
+    for T in (0.7, 1.0, 1.6):
+        z = (l64 - l64.max()) / T
+        lse = math.log(np.sum(np.exp(z)))
+        for t in [int(np.argmax(logits)), int(np.argmin(logits)), 17, 4999]:
+            want = max(z[t] - lse, -30.0)
+            got = oracle.full_vocab_token_logprob(logits, t, T)
+            assert abs(got - want) <= 2e-5 * max(1.0, abs(want)), (T, t, got, want)
+    # floor at -30: an id 200 nats below the maximum
+    x = np.array([0.0, -200.0, 0.0], dtype=np.float32)
+    assert oracle.full_vocab_token_logprob(x, 1, 1.0) == -30.0
+    assert oracle.full_vocab_token_logprob(x, 0, 1.0) == float(np.float32(math.log(0.5)))
+    # out of range id, greedy temperature
+    assert oracle.full_vocab_token_logprob(x, 3, 1.0) == -30.0
+    assert oracle.full_vocab_token_logprob(x, 0, 0.0) == 0.0        # first maximum
+    assert oracle.full_vocab_token_logprob(x, 2, 0.0) == -np.inf    # tie loses to id 0
+    # -inf logits contribute nothing; an all -inf row has no finite mass → -30
+    y = np.array([-np.inf, 1.0, -np.inf], dtype=np.float32)
+    assert oracle.full_vocab_token_logprob(y, 1, 0.9) == 0.0
+    assert oracle.full_vocab_token_logprob(np.full(4, -np.inf, np.float32), 1, 1.0) == -30.0
+
+
+# --- MTP verify: float64 statement of the function-level law --------------------
+
+
+def _dist64(logits, mp):
+    ids, p, margin = law64(logits, mp)
+    return ids, p / p.sum(), margin
+
+
+def mtp64(tgt, dft, dids, tmp, dmp, us):
+    """Float64 statement of one sequence's verify step: accept iff
+    u < min(1, P(d) / q') with q' = exp(ln q * Td/Tt) (temperatures differing
+    by > 1e-6), ln q = max(ln max(Q(d), 1e-37), -30)
+    (crates/ax-engine-mlx/src/runner/mod.rs:12388-12419); on reject the
+    residual max(P - Q, 0) over the ascending-id union, normalised, drawn with
+    the tail uniform, or the target itself when the residual is empty
+    (crates/ax-engine-mlx/src/sampling.rs:733-752); all accepted: the bonus
+    draw of target row D (runner/mod.rs:9732-9775).  Returns (ids, smallest
+    decision margin)."""
+    D = len(dids)
+    Tt, Td = tmp.temperature, dmp.temperature
+    out, margin = [], np.inf
+    for i in range(D):
+        tid, tp, tm = _dist64(tgt[i], tmp)
+        did, dq, dm = _dist64(dft[i], dmp)
+        margin = min(margin, tm, dm)
+        d = int(dids[i])
+        q = float(dq[did == d].sum())
+        p = float(tp[tid == d].sum())
+        lnq = max(math.log(max(q, 1e-37)), -30.0)
+        lps = lnq * (Td / Tt) if (Td > 0 and Tt > 0 and abs(Td - Tt) > 1e-6) else lnq
+        acc = min(p / max(math.exp(lps), 1e-37), 1.0)
+        u = float(us[i])
+        if u < 1.0:
+            margin = min(margin, abs(u - acc))
+        if u < acc:
+            out.append(d)
+            continue
+        P = dict(zip(tid.tolist(), tp.tolist()))
+        Q = dict(zip(did.tolist(), dq.tolist()))
+        keys = sorted(set(P) | set(Q))
+        r = []
+        for k in keys:
+            diff = P.get(k, 0.0) - Q.get(k, 0.0)
+            if k in P and k in Q and diff != 0.0:
+                margin = min(margin, abs(diff))
+            r.append(max(diff, 0.0))
+        r = np.array(r)
+        if r.sum() > 0.0:
+            tok, m2 = draw64(np.array(keys), r, float(us[D]))
+        else:
+            tok, m2 = draw64(tid, tp, float(us[D]))
+        return out + [tok], min(margin, m2)
+    bid, bp, bm = law64(tgt[D], tmp)
+    tok, m2 = draw64(bid, bp, float(us[D]))
+    return out + [tok], min(margin, bm, m2)
+
+
+def _rand_mp(rs):
+    mp = MlxSamplingParams.new(float(rs.choice([0.6, 0.9, 1.3])), float(rs.choice([1.0, 0.95, 0.7])),
+                               int(rs.choice([0, 0, 2, 3])))
+    return mp.with_min_p(None if rs.random() < 0.6 else float(rs.choice([0.05, 0.2])))
+
+
+@pytest.mark.parametrize("seed", range(30))
+def test_mtp_verify_matches_float64_law(oracle, seed):
+    """axo_mtp_verify_seq on V <= 8 against the float64 statement above, over
+    random uniforms, wherever every decision has a margin > 1e-4."""
+    from ax_sampler.params import pack_params
+
+    rs = np.random.default_rng(1000 + seed)
+    V = int(rs.integers(3, 9))
+    D = int(rs.integers(1, 4))
+    tgt = rs.normal(0, 1.5, (D + 1, V)).astype(np.float32)
+    if seed % 5 == 0:
+        dft = tgt[:D].copy()           # draft == target: residual empty → target
+    else:
+        dft = (tgt[:D] + rs.normal(0, 0.7, (D, V))).astype(np.float32)
+    tmp = _rand_mp(rs)
+    dmp = tmp if seed % 5 == 0 else _rand_mp(rs)
+    N = 400
+    dids = rs.integers(0, V, (N, D)).astype(np.uint32)
+    us = rs.random((N, D + 1)).astype(np.float32)
+    us[: N // 8, :D] = 0.0            # accept everything → bonus
+    us[N // 8: N // 4, 0] = 1.0       # reject the first draft
+    T = np.ascontiguousarray(np.broadcast_to(tgt, (N, D + 1, V)))
+    Dr = np.ascontiguousarray(np.broadcast_to(dft, (N, D, V)))
+    out_ids, out_n, acc, fl = oracle.mtp_verify_batch(T, Dr, 0, N, D, V, V, dids,
+                                                      pack_params([tmp] * N), pack_params([dmp] * N),
+                                                      uniforms=us, nthreads=4)
+    checked = 0
+    for b in range(N):
+        want, margin = mtp64(tgt, dft, dids[b], tmp, dmp, us[b])
+        if margin < 1e-4:
+            continue
+        got = out_ids[b, : out_n[b]].tolist()
+        assert got == want, (seed, b, got, want, us[b].tolist(), dids[b].tolist())
+        assert int(acc[b]) == min(len(want) - 1, D) and fl[b] & 0x80000000 == 0
+        checked += 1
+    assert checked >= N // 2, (seed, checked)
+
+
+@pytest.mark.parametrize("filtered", [False, True])
+def test_mtp_first_token_follows_the_target_law(oracle, filtered):
+    """Speculative sampling's defining property: with equal temperatures and
+    the draft token drawn from Q, the first emitted token (accepted draft or
+    residual) is distributed as the target law P.  chi^2 over 40,000
+    sequences."""
+    from ax_sampler.params import pack_params
+
+    rs = np.random.default_rng(77 + filtered)
+    V, D, N = 6, 2, 40000
+    tgt = rs.normal(0, 1.0, (D + 1, V)).astype(np.float32)
+    dft = (tgt[:D] + rs.normal(0, 0.8, (D, V))).astype(np.float32)
+    mp = MlxSamplingParams.new(0.8, 0.9 if filtered else 1.0, 4 if filtered else 0)
+    qi, qp = oracle.token_distribution(dft[0], P(mp))
+    qi1, qp1 = oracle.token_distribution(dft[1], P(mp))
+    ud = rs.random((N, 2)).astype(np.float32)
+    dids = np.zeros((N, D), np.uint32)
+    for b in range(N):
+        dids[b, 0] = oracle.sample_from_distribution(qi, qp, float(ud[b, 0]))
+        dids[b, 1] = oracle.sample_from_distribution(qi1, qp1, float(ud[b, 1]))
+    us = rs.random((N, D + 1)).astype(np.float32)
+    T = np.ascontiguousarray(np.broadcast_to(tgt, (N, D + 1, V)))
+    Dr = np.ascontiguousarray(np.broadcast_to(dft, (N, D, V)))
+    pp = pack_params([mp] * N)
+    out_ids, out_n, _, _ = oracle.mtp_verify_batch(T, Dr, 0, N, D, V, V, dids, pp, pp, uniforms=us,
+                                                   nthreads=8)
+    pid, pv, _ = _dist64(tgt[0], mp)
+    first = out_ids[:, 0]
+    assert set(np.unique(first).tolist()) <= set(pid.tolist())
+    chi2 = sum((np.count_nonzero(first == i) - N * q) ** 2 / (N * q) for i, q in zip(pid, pv))
+    assert chi2 < 25.0, chi2  # <= 5 dof, p ~ 1e-4
