@@ -51,9 +51,11 @@ HIPCC_FLAGS = [
 EXPORTS = (
     "axs_abi_version",
     "axs_last_error",
+    "axs_set_error_handler",
     "axs_context_create",
     "axs_context_destroy",
     "axs_sample_batch",
+    "axs_sample_batch_host",
     "axs_argmax_batch",
     "axs_mtp_verify",
     "axs_timing_enable",
@@ -164,12 +166,16 @@ def lib():
             L.axs_abi_version.argtypes = []
             L.axs_last_error.restype = C.c_char_p
             L.axs_last_error.argtypes = []
+            L.axs_set_error_handler.restype = None
+            L.axs_set_error_handler.argtypes = [vp, vp]
             L.axs_context_create.restype = i32
             L.axs_context_create.argtypes = [i32, i32, i32, C.POINTER(vp)]
             L.axs_context_destroy.restype = i32
             L.axs_context_destroy.argtypes = [vp]
             L.axs_sample_batch.restype = i32
             L.axs_sample_batch.argtypes = [vp, C.POINTER(BatchDesc), C.POINTER(Outputs), vp]
+            L.axs_sample_batch_host.restype = i32
+            L.axs_sample_batch_host.argtypes = [vp, C.POINTER(BatchDesc), C.POINTER(Outputs)]
             L.axs_argmax_batch.restype = i32
             L.axs_argmax_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_mtp_verify.restype = i32

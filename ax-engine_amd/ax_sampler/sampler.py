@@ -256,6 +256,83 @@ class HipSampler:
         _abi.check(self.L.axs_sample_batch(self.ctx, C.byref(d), C.byref(o), self._stream(stream)))
         return SampleResult(out_ids, out_lp, out_flags, kept, kept_n, tuple(keep))
 
+    def sample_host(
+        self,
+        logits: np.ndarray,
+        params,
+        *,
+        history: Optional[Sequence[Sequence[int]]] = None,
+        mask_words: Optional[np.ndarray] = None,
+        bias: Optional[Sequence[Tuple[Sequence[int], Sequence[float]]]] = None,
+        uniforms: Optional[np.ndarray] = None,
+        logprobs: bool = False,
+        kept_cap: int = 0,
+        bf16: bool = False,
+    ):
+        """One batched sampling step over HOST logits (``axs_sample_batch_host``):
+        the engine-level boundary, whose requests carry their logits as host
+        vectors (crates/ax-engine-core/src/sampling.rs:78).  ``logits`` is a
+        [B, V] float32 array (or uint16 bf16 bits with ``bf16=True``); every
+        other argument is host data too.  Synchronous; returns numpy arrays
+        (token ids, logprobs or None, flags, kept ids or None, kept counts or
+        None)."""
+        lg = np.ascontiguousarray(logits)
+        if lg.ndim != 2:
+            raise ValueError(f"logits must be [B, V], got {lg.shape}")
+        if bf16 and lg.dtype != np.uint16:
+            raise TypeError("bf16 logits are passed as uint16 bits")
+        if not bf16 and lg.dtype != np.float32:
+            raise TypeError("logits must be float32 (or uint16 bf16 bits with bf16=True)")
+        B, V = lg.shape
+        keep = [lg]
+        d = _abi.BatchDesc()
+        d.logits = lg.ctypes.data
+        d.dtype = _abi.AXS_DTYPE_BF16 if bf16 else _abi.AXS_DTYPE_F32
+        d.batch, d.vocab, d.row_stride = B, V, V
+        pp = params if isinstance(params, np.ndarray) else pack_params(list(params))
+        assert pp.dtype == PARAMS_DTYPE and pp.size == B
+        pp = np.ascontiguousarray(pp)
+        keep.append(pp)
+        d.params = pp.ctypes.data
+        if history is not None:
+            if len(history) != B:
+                raise ValueError("history must have one entry per row")
+            flat, off = _csr(history)
+            keep += [flat, off]
+            d.history, d.history_offsets, d.history_len = flat.ctypes.data, off.ctypes.data, int(off[-1])
+        if mask_words is not None:
+            mw = np.ascontiguousarray(mask_words, dtype=np.uint32)
+            keep.append(mw)
+            d.mask_words, d.mask_stride = mw.ctypes.data, int(mw.shape[-1])
+        if bias is not None:
+            if len(bias) != B:
+                raise ValueError("bias must have one entry per row")
+            ids, off = _csr([b[0] for b in bias])
+            vals = np.zeros(max(int(off[-1]), 1), dtype=np.float32)
+            for i, b in enumerate(bias):
+                if len(b[1]):
+                    vals[off[i]: off[i + 1]] = np.asarray(b[1], dtype=np.float32)
+            keep += [ids, vals, off]
+            d.bias_ids, d.bias_values, d.bias_offsets = ids.ctypes.data, vals.ctypes.data, off.ctypes.data
+            d.bias_len = int(off[-1])
+        if uniforms is not None:
+            un = np.ascontiguousarray(uniforms, dtype=np.float32)
+            keep.append(un)
+            d.uniforms = un.ctypes.data
+        tid = np.zeros(B, dtype=np.uint32)
+        fl = np.zeros(B, dtype=np.uint32)
+        lp = np.zeros(B, dtype=np.float32) if logprobs else None
+        kid = np.zeros((B, kept_cap), dtype=np.uint32) if kept_cap else None
+        kc = np.zeros(B, dtype=np.uint32) if kept_cap else None
+        o = _abi.Outputs()
+        o.token_ids, o.flags = tid.ctypes.data, fl.ctypes.data
+        o.logprobs = None if lp is None else lp.ctypes.data
+        o.kept_ids = None if kid is None else kid.ctypes.data
+        o.kept_count = None if kc is None else kc.ctypes.data
+        o.kept_cap = kept_cap
+        _abi.check(self.L.axs_sample_batch_host(self.ctx, C.byref(d), C.byref(o)))
+        return tid, lp, fl, kid, kc
+
     def argmax(self, logits, logprobs: bool = True, stream=None):
         """Greedy ids (first maximum, NaN skipped) and -ln sum exp(l - max)."""
         torch = _torch()
@@ -387,69 +464,85 @@ def recent_repetition_tokens(prompt: Sequence[int], generated: Sequence[int],
 class HipTokenSampler:
     """``TokenSampler`` (crates/ax-engine-core/src/sampling.rs:90-92) on the GPU.
 
-    Requests with logits are sampled with their own ``SamplingParams`` by the
-    HIP library (greedy rows: first-maximum argmax with logprob -ln sum
-    exp(l - max); sampled rows: the full filter chain, draw from
-    Philox(seed, request_id, generated_len)).  Invalid logits — a processed
-    maximum that is not finite, or any NaN, as the core sampler's total_cmp
-    maximum sees them (core sampling.rs:172-178) — give token 0 with
-    ``StopReason.ERROR`` and no logprob.  Requests without logits keep the
-    core stub behaviour (previous_token + 1, logprob 0).  Ties: this sampler
-    keeps the MLX sampler's first maximum, where the core DeterministicSampler
-    keeps the last one.
+    The requests that carry logits are sampled in one call of the host-pointer
+    entry point (``axs_sample_batch_host``: the logits are host vectors at this
+    level, core sampling.rs:78), each with its own ``SamplingParams`` under
+    the MLX law (greedy rows: first-maximum argmax with the core sampler's
+    logprob -ln sum exp(l - max), reproduced from its sequential f32 sum;
+    sampled rows: the full filter chain, drawn from Philox(seed, request_id,
+    generated_len)).  The core ``DeterministicSampler``'s contract otherwise
+    (core sampling.rs:97-136):
+      * one ``SampledToken`` per request, in order;
+      * invalid logits — empty, or a maximum under ``f32::total_cmp`` that is
+        not finite (a +NaN ranks above +inf there, a -NaN below -inf; core
+        sampling.rs:172-178) — give token 0, ``StopReason.ERROR``, no logprob;
+      * ``MaxOutputTokens`` when ``generated_len + 1 >= max_output_tokens``
+        (saturating);
+      * requests without logits keep the core stub: ``previous_token + 1``
+        (saturating at 0xFFFFFFFF), logprob 0.
+    Ties: this sampler keeps the MLX sampler's first maximum, where the core
+    DeterministicSampler keeps the last one.  Rows of different widths are
+    sampled in separate calls.
     """
 
     def __init__(self, sampler: HipSampler):
         self.sampler = sampler
 
+    @staticmethod
+    def _valid(arr: np.ndarray) -> bool:
+        if arr.size == 0:
+            return False
+        bits = arr.view(np.uint32)
+        nan = np.isnan(arr)
+        if np.any(nan & ((bits >> np.uint32(31)) == 0)):
+            return False  # a +NaN is the total_cmp maximum
+        rest = arr[~nan]
+        return rest.size > 0 and bool(np.isfinite(rest.max()))
+
     def sample(self, inp: SamplerInput) -> List[SampledToken]:
-        torch = _torch()
         reqs = inp.requests
-        out: List[Optional[SampledToken]] = [None] * len(reqs)
         rows, idx = [], []
         for i, rq in enumerate(reqs):
             if rq.logits is None:
                 continue
-            arr = np.asarray(rq.logits, dtype=np.float32)
-            mx = arr.max() if arr.size else np.float32(np.nan)
-            if arr.size == 0 or np.isnan(arr).any() or not np.isfinite(mx):
+            arr = np.ascontiguousarray(rq.logits, dtype=np.float32)
+            if not self._valid(arr):
                 continue  # invalid: token 0 + Error below
             rows.append(arr)
             idx.append(i)
         tokens, lps = {}, {}
-        if rows:
-            V = max(r.size for r in rows)
-            if any(r.size != V for r in rows):
-                # rows of different widths are sampled as separate batches
-                groups = {}
-                for r, i in zip(rows, idx):
-                    groups.setdefault(r.size, []).append((r, i))
-            else:
-                groups = {V: list(zip(rows, idx))}
-            for V, items in groups.items():
-                mat = np.stack([r for r, _ in items])
-                ids = [i for _, i in items]
-                mps = [reqs[i].sampling_params.to_mlx() for i in ids]
-                hist = [list(reqs[i].recent_tokens) for i in ids]
-                seeds = [reqs[i].sampling_params.seed for i in ids]
-                us = philox_uniforms(seeds, [reqs[i].request_id for i in ids],
-                                     [reqs[i].generated_len for i in ids])
-                t = torch.from_numpy(mat).to(self.sampler.device)
-                res = self.sampler.sample(t, pack_params(mps, seeds), history=hist, uniforms=us,
-                                          logprobs=True)
-                tid, lp, fl, _, _ = res.numpy()
-                for k, i in enumerate(ids):
-                    if fl[k] & _abi.FLAG_ERROR:
-                        continue
-                    tokens[i] = int(tid[k])
-                    lps[i] = float(lp[k])
+        groups = {}
+        for r, i in zip(rows, idx):
+            groups.setdefault(r.size, []).append((r, i))
+        for V, items in groups.items():
+            mat = np.stack([r for r, _ in items])
+            ids = [i for _, i in items]
+            # the core sampler penalises every recent token it is given (the
+            # engine has already cut them to the window,
+            # crates/ax-engine-core/src/engine.rs:1180-1197)
+            mps = [reqs[i].sampling_params.to_mlx() for i in ids]
+            for mp in mps:
+                mp.repetition_context_size = None
+            hist = [list(reqs[i].recent_tokens) for i in ids]
+            seeds = [reqs[i].sampling_params.seed for i in ids]
+            us = philox_uniforms(seeds, [reqs[i].request_id for i in ids],
+                                 [reqs[i].generated_len for i in ids])
+            tid, lp, fl, _, _ = self.sampler.sample_host(mat, pack_params(mps, seeds), history=hist,
+                                                         uniforms=us, logprobs=True)
+            for k, i in enumerate(ids):
+                if fl[k] & _abi.FLAG_ERROR:
+                    continue
+                tokens[i] = int(tid[k])
+                lps[i] = float(lp[k])
+        out: List[SampledToken] = []
         for i, rq in enumerate(reqs):
             invalid = rq.logits is not None and i not in tokens
             if invalid:
                 tok, lp, stop = 0, None, StopReason.ERROR
             else:
-                tok = tokens.get(i, (rq.previous_token + 1) & 0xFFFFFFFF)
+                tok = tokens.get(i, min(rq.previous_token + 1, 0xFFFFFFFF))
                 lp = lps.get(i, 0.0)
-                stop = StopReason.MAX_OUTPUT_TOKENS if rq.generated_len + 1 >= rq.max_output_tokens else None
-            out[i] = SampledToken(rq.request_id, tok, stop, lp)
-        return out  # type: ignore[return-value]
+                stop = (StopReason.MAX_OUTPUT_TOKENS
+                        if min(rq.generated_len + 1, 0xFFFFFFFF) >= rq.max_output_tokens else None)
+            out.append(SampledToken(rq.request_id, tok, stop, lp))
+        return out

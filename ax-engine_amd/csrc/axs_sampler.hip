@@ -169,6 +169,8 @@ struct KArgs {
     int32_t want_logprob;
     int32_t vec;          // rows are 16-byte aligned: vector loads
     int32_t inplace;      // k_row: a row's exact path in its own workgroup (else listed)
+    int32_t exact_lp;     // greedy rows' logprob: the core sampler's sequential sum (exact path)
+    int32_t pad0;
     int64_t stride;
     const axs_sampling_params* params;
     const axs_sampling_params* params2;
@@ -987,6 +989,18 @@ __device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_s
         return false;
     }
     if (mode == M_GREEDY) {
+        if (a.exact_lp && a.want_logprob && isfinite(m)) {
+            // the core sampler's logprob -ln(sum exp(l - max)), its f32 sum
+            // taken in index order over finite l
+            // (crates/ax-engine-core/src/sampling.rs:177-190): the exact path's
+            // index-order running sum of an untruncated law at T = 1
+            if (INPLACE) {
+                *xs = exact_state(a, r, p, m, 1.0f, M_GREEDY, false, am);
+                return true;
+            }
+            if (tid == 0) list_exact(a, r, p, m, 1.0f, M_GREEDY, false, am);
+            return false;
+        }
         if (tid == 0) {
             const float lp = (a.want_logprob && isfinite(m) && gs > 0.0) ? (float)(-log(gs)) : NAN;
             write_row(a, r, am, lp, AXS_FLAG_GREEDY);
@@ -1403,7 +1417,9 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
     const uint32_t mode = c.mode;
     const float inv = __fdiv_rn(1.0f, c.p.temperature);
     const bool gather = mode == M_MINP && isfinite(inv);
-    const bool gsum_on = mode == M_GREEDY && a.want_logprob;
+    // the approximate greedy logprob of the stream (rows that take the exact
+    // path for it need none)
+    const bool gsum_on = mode == M_GREEDY && a.want_logprob && !a.exact_lp;
     const float thr = gather ? __fsub_rn(ln_f32(c.p.min_p), 1e-3f) : 0.0f;
     const uint32_t sflags = (c.err || (c.any_proc && L.err)) ? CS_ERROR : 0u;
 
@@ -1554,8 +1570,11 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
         mrun = mm;
         set_pre();
     }
-    // claims the next chunk for this wave
-    auto grab = [&]() {
+    // claims the next chunk for this wave; a greedy logprob row takes every
+    // NW-th chunk in order instead, so that each lane's sum runs over the same
+    // elements in the same order on every call (a reproducible logprob)
+    auto grab = [&](uint32_t cur) {
+        if (gsum_on) return cur + 2u * NW;
         uint32_t ch = 0;
         if (lane == 0) ch = atomicAdd(&SL.next, 1u);
         return (uint32_t)__builtin_amdgcn_readfirstlane((int)ch);
@@ -1568,7 +1587,7 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
             set_pre();
         }
         process(T, ch);
-        ch = grab();
+        ch = grab(ch);
         load(T, ch);
         if (gather) raise();
     };
@@ -2041,7 +2060,9 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     const uint32_t mode = c.mode;
     const float inv = __fdiv_rn(1.0f, c.p.temperature);
     const bool gather = mode == M_MINP && isfinite(inv);
-    const bool gsum_on = mode == M_GREEDY && a.want_logprob;
+    // the approximate greedy logprob of the stream (rows that take the exact
+    // path for it need none)
+    const bool gsum_on = mode == M_GREEDY && a.want_logprob && !a.exact_lp;
     const float thr = gather ? __fsub_rn(ln_f32(c.p.min_p), 1e-3f) : 0.0f;
     const uint32_t sflags = (c.err || (SL.err & RERR_BIAS)) ? CS_ERROR : 0u;
     // Processors that can only lower a logit (repetition >= 1, presence and
@@ -2335,7 +2356,11 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
         mrun = fmaxf(mrun, fmaxf(wm, ord2f(g)));
         set_pre();
     };
-    auto grab = [&]() {
+    // the next chunk for this wave: claimed, or, for a greedy logprob row,
+    // every NW-th chunk in order (each lane's sum then runs over the same
+    // elements in the same order on every call: a reproducible logprob)
+    auto grab = [&](uint32_t cur) {
+        if (gsum_on) return cur + 2u * NW;
         uint32_t ch = 0;
         if (lane == 0) ch = atomicAdd(&SL.next, 1u);
         return (uint32_t)__builtin_amdgcn_readfirstlane((int)ch);
@@ -2344,7 +2369,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     auto step = [&](Tile<DT, TV, MASK>& T, uint32_t& ch) __attribute__((always_inline)) {
         if (bound && mrun == -INFINITY) raise(wave_max_dpp(tile_max(T, ch)));
         process(T, ch);
-        ch = grab();
+        ch = grab(ch);
         load(T, ch);
         if (bound) raise(wave_max_dpp(tm));
     };
@@ -2977,6 +3002,21 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     __threadfence_block();
     __syncthreads();  // every S store complete before the decisions read S
 
+    if (rs.mode == M_GREEDY) {
+        // greedy row listed for its logprob: -ln of the index-order sum
+        // (crates/ax-engine-core/src/sampling.rs:179-190); the token is the
+        // first maximum found by the stream
+        if (tid == 0) {
+            const float F0 = S[V - 1];
+            const float lp = (F0 > 0.0f && isfinite(F0)) ? -ln_f32(F0) : NAN;
+            const uint32_t flags = AXS_FLAG_GREEDY | AXS_FLAG_EXACT_PATH;
+            write_row(a, r, rs.amax, lp, flags);
+            write_single_kept(a, r, rs.amax);
+            if (a.ws_kept_id) a.rstate[r].flags = flags;
+        }
+        return;
+    }
+
     // index-order rows: the kept-set size and the ordered kept lists, by the
     // whole block
     uint32_t dkept = 0, dlist = 0;
@@ -3356,9 +3396,22 @@ using namespace axs;
 namespace {
 
 thread_local std::string g_last_error;
+std::mutex g_handler_mu;
+axs_error_handler_func g_handler = nullptr;
+void* g_handler_data = nullptr;
 
+// Records the message of a failed call for this thread and passes it to the
+// registered error handler, on this thread.
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
+    axs_error_handler_func h;
+    void* hd;
+    {
+        std::lock_guard<std::mutex> lk(g_handler_mu);
+        h = g_handler;
+        hd = g_handler_data;
+    }
+    if (h) h(g_last_error.c_str(), hd);
     return code;
 }
 
@@ -3395,6 +3448,19 @@ struct axs_context {
     uint32_t* mtp_tok;  // per-row tokens of the MTP sampler pass
     bool timing;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev[AXS_KERNEL_COUNT];
+    // Calls are serialised: the lock covers each call's enqueue, and a call
+    // on another stream than the previous one first waits for the previous
+    // call's work (done_ev), so two streams never run on the workspace at
+    // once.
+    std::mutex mu;
+    hipEvent_t done_ev;
+    hipStream_t last_stream;
+    bool has_last;
+    // axs_sample_batch_host: the context's own stream and device staging
+    // for host inputs and outputs, grown on demand
+    hipStream_t own_stream;
+    void* stage[16];
+    size_t stage_cap[16];
 };
 
 namespace {
@@ -3426,6 +3492,10 @@ void clear_events(axs_context* c);
 
 void free_ctx(axs_context* c) {
     clear_events(c);
+    for (int i = 0; i < 16; ++i)
+        if (c->stage[i]) (void)hipFree(c->stage[i]);
+    if (c->done_ev) (void)hipEventDestroy(c->done_ev);
+    if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     void* ptrs[] = {c->cstat, c->pool, c->rstate,  c->exact_rows, c->exact_count,
                     c->row_done, c->dense, c->ckey, c->ckey2, c->tmp64, c->sbuf, c->bend,
                     c->kept_id, c->kept_p, c->mtp_tok};
@@ -3556,19 +3626,14 @@ void launch_stream_tv(const KArgs& a, hipStream_t s) {
     else hipLaunchKernelGGL((k_stream<DT, 4, false, NT, SEGMAX, FAST>), grid, dim3(NT), 0, s, a);
 }
 
-// one row per 1024-thread workgroup; AXS_ROW_TV (4 or 8, tuning) vectors per
-// lane in each chunk
-template <int DT, bool FAST, int TV>
-void launch_row_tv(const KArgs& a, hipStream_t s) {
+// one row per 1024-thread workgroup, 4 vectors per lane in each chunk (8:
+// +4 us at C3, 2: +0.5 us, measured)
+template <int DT, bool FAST>
+void launch_row(const KArgs& a, hipStream_t s) {
+    constexpr int TV = 4;
     dim3 grid((unsigned)(((a.nrows + 7) / 8) * 8));
     if (a.mask) hipLaunchKernelGGL((k_row<DT, TV, true, FAST>), grid, dim3(RT), 0, s, a);
     else hipLaunchKernelGGL((k_row<DT, TV, false, FAST>), grid, dim3(RT), 0, s, a);
-}
-template <int DT, bool FAST>
-void launch_row(const KArgs& a, hipStream_t s) {
-    static const int tv = env_int("AXS_ROW_TV", 4);
-    if (tv == 4) launch_row_tv<DT, FAST, 4>(a, s);
-    else launch_row_tv<DT, FAST, 8>(a, s);
 }
 
 // fast: 16-byte aligned rows of whole vectors (every segment end, a multiple
@@ -3665,6 +3730,49 @@ int run_pipeline(axs_context* c, KArgs& a, const Plan& pl, hipStream_t s) {
     return AXS_OK;
 }
 
+// A call's work on stream s follows the previous call's when that ran on
+// another stream (not while s is being captured into a graph: the previous
+// call's event is then outside the capture).
+int order_begin(axs_context* c, hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    AXS_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+    if (c->has_last && c->last_stream != s && cs == hipStreamCaptureStatusNone)
+        AXS_HIP_CHECK(hipStreamWaitEvent(s, c->done_ev, 0));
+    return AXS_OK;
+}
+int order_end(axs_context* c, hipStream_t s) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    AXS_HIP_CHECK(hipStreamIsCapturing(s, &cs));
+    if (cs != hipStreamCaptureStatusNone) {
+        c->has_last = false;
+        return AXS_OK;
+    }
+    AXS_HIP_CHECK(hipEventRecord(c->done_ev, s));
+    c->last_stream = s;
+    c->has_last = true;
+    return AXS_OK;
+}
+
+// Device staging slot i of at least n bytes (grown, never shrunk).
+int stage_at(axs_context* c, int i, size_t n, void** out) {
+    if (n == 0) n = 16;
+    if (c->stage_cap[i] < n) {
+        if (c->stage[i]) {
+            AXS_HIP_CHECK(hipStreamSynchronize(c->own_stream));
+            AXS_HIP_CHECK(hipFree(c->stage[i]));
+            c->stage[i] = nullptr;
+            c->stage_cap[i] = 0;
+        }
+        void* q = nullptr;
+        hipError_t e = hipMalloc(&q, n + 256);
+        if (e != hipSuccess) return fail(AXS_E_HIP, std::string("hipMalloc (staging): ") + hipGetErrorString(e));
+        c->stage[i] = q;
+        c->stage_cap[i] = n;
+    }
+    *out = c->stage[i];
+    return AXS_OK;
+}
+
 uint32_t next_pow2_h(uint32_t n) {
     uint32_t p = 1;
     while (p < n) p <<= 1;
@@ -3678,6 +3786,12 @@ extern "C" {
 int axs_abi_version(void) { return AXS_ABI_VERSION; }
 
 const char* axs_last_error(void) { return g_last_error.c_str(); }
+
+void axs_set_error_handler(axs_error_handler_func handler, void* data) {
+    std::lock_guard<std::mutex> lk(g_handler_mu);
+    g_handler = handler;
+    g_handler_data = data;
+}
 
 int axs_context_create(int device, int max_batch, int max_vocab, axs_context** out) {
     if (!out) return fail(AXS_E_INVALID, "out is NULL");
@@ -3709,6 +3823,11 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
         return rc;
     }
     c->ex_done = c->row_done + R;
+    if (hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess ||
+        hipEventCreateWithFlags(&c->done_ev, hipEventDisableTiming) != hipSuccess) {
+        free_ctx(c);
+        return fail(AXS_E_HIP, "creating the context's stream and event failed");
+    }
     // the counters start at zero; every call leaves them at zero again
     if (hipMemset(c->row_done, 0, (R + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(c->exact_count, 0, sizeof(uint32_t)) != hipSuccess ||
@@ -3728,7 +3847,12 @@ int axs_context_destroy(axs_context* ctx) {
     return AXS_OK;
 }
 
-int axs_sample_batch(axs_context* ctx, const axs_batch_desc* d, const axs_outputs* o, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// Validation shared by the device- and host-pointer sampling entry points.
+int check_batch(axs_context* ctx, const axs_batch_desc* d, const axs_outputs* o) {
     if (!ctx || !d || !o) return fail(AXS_E_INVALID, "ctx, desc and outputs must be non-NULL");
     if (!d->logits || !d->params || !o->token_ids)
         return fail(AXS_E_INVALID, "logits, params and token_ids must be non-NULL");
@@ -3744,8 +3868,111 @@ int axs_sample_batch(axs_context* ctx, const axs_batch_desc* d, const axs_output
     if (d->bias_ids && (!d->bias_values || !d->bias_offsets || d->bias_len < 0))
         return fail(AXS_E_INVALID, "bias_ids needs bias_values, bias_offsets and bias_len");
     if (o->kept_ids && o->kept_cap < 1) return fail(AXS_E_INVALID, "kept_ids needs kept_cap >= 1");
+    return AXS_OK;
+}
+
+int sample_batch_locked(axs_context* ctx, const axs_batch_desc* d, const axs_outputs* o, hipStream_t s);
+
+}  // namespace
+
+extern "C" {
+
+int axs_sample_batch(axs_context* ctx, const axs_batch_desc* d, const axs_outputs* o, void* stream) {
+    int rc = check_batch(ctx, d, o);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
     DevGuard g(ctx->device);
     hipStream_t s = (hipStream_t)stream;
+    if ((rc = order_begin(ctx, s))) return rc;
+    if ((rc = sample_batch_locked(ctx, d, o, s))) return rc;
+    return order_end(ctx, s);
+}
+
+int axs_sample_batch_host(axs_context* ctx, const axs_batch_desc* hd, const axs_outputs* ho) {
+    int rc = check_batch(ctx, hd, ho);
+    if (rc) return rc;
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DevGuard g(ctx->device);
+    hipStream_t s = ctx->own_stream;
+    if ((rc = order_begin(ctx, s))) return rc;
+    const int B = hd->batch, V = hd->vocab;
+    const size_t es = hd->dtype == AXS_DTYPE_BF16 ? 2 : 4;
+    axs_batch_desc d = *hd;
+    axs_outputs o = *ho;
+    void* p = nullptr;
+    auto up = [&](int slot, const void* src, size_t n, void** dst) -> int {
+        int r = stage_at(ctx, slot, n, dst);
+        if (r) return r;
+        if (n) AXS_HIP_CHECK(hipMemcpyAsync(*dst, src, n, hipMemcpyHostToDevice, s));
+        return AXS_OK;
+    };
+    // logits, packed to row stride = vocab
+    if ((rc = stage_at(ctx, 0, (size_t)B * V * es, &p))) return rc;
+    AXS_HIP_CHECK(hipMemcpy2DAsync(p, (size_t)V * es, hd->logits, (size_t)hd->row_stride * es, (size_t)V * es,
+                                   (size_t)B, hipMemcpyHostToDevice, s));
+    d.logits = p;
+    d.row_stride = V;
+    if ((rc = up(1, hd->params, (size_t)B * sizeof(axs_sampling_params), &p))) return rc;
+    d.params = (const axs_sampling_params*)p;
+    if (hd->history) {
+        if ((rc = up(2, hd->history, (size_t)hd->history_len * 4, &p))) return rc;
+        d.history = (const uint32_t*)p;
+        if ((rc = up(3, hd->history_offsets, (size_t)(B + 1) * 8, &p))) return rc;
+        d.history_offsets = (const int64_t*)p;
+    }
+    if (hd->mask_words) {
+        if ((rc = up(4, hd->mask_words, (size_t)B * hd->mask_stride * 4, &p))) return rc;
+        d.mask_words = (const uint32_t*)p;
+    }
+    if (hd->bias_ids) {
+        if ((rc = up(5, hd->bias_ids, (size_t)hd->bias_len * 4, &p))) return rc;
+        d.bias_ids = (const uint32_t*)p;
+        if ((rc = up(6, hd->bias_values, (size_t)hd->bias_len * 4, &p))) return rc;
+        d.bias_values = (const float*)p;
+        if ((rc = up(7, hd->bias_offsets, (size_t)(B + 1) * 8, &p))) return rc;
+        d.bias_offsets = (const int64_t*)p;
+    }
+    if (hd->uniforms) {
+        if ((rc = up(8, hd->uniforms, (size_t)B * 4, &p))) return rc;
+        d.uniforms = (const float*)p;
+    }
+    // device outputs
+    void *dt = nullptr, *dl = nullptr, *df = nullptr, *dk = nullptr, *dc = nullptr;
+    if ((rc = stage_at(ctx, 9, (size_t)B * 4, &dt))) return rc;
+    o.token_ids = (uint32_t*)dt;
+    if (ho->logprobs) {
+        if ((rc = stage_at(ctx, 10, (size_t)B * 4, &dl))) return rc;
+        o.logprobs = (float*)dl;
+    }
+    if (ho->flags) {
+        if ((rc = stage_at(ctx, 11, (size_t)B * 4, &df))) return rc;
+        o.flags = (uint32_t*)df;
+    }
+    if (ho->kept_ids) {
+        if ((rc = stage_at(ctx, 12, (size_t)B * ho->kept_cap * 4, &dk))) return rc;
+        o.kept_ids = (uint32_t*)dk;
+    }
+    if (ho->kept_count) {
+        if ((rc = stage_at(ctx, 13, (size_t)B * 4, &dc))) return rc;
+        o.kept_count = (uint32_t*)dc;
+    }
+    if ((rc = sample_batch_locked(ctx, &d, &o, s))) return rc;
+    AXS_HIP_CHECK(hipMemcpyAsync(ho->token_ids, dt, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+    if (ho->logprobs) AXS_HIP_CHECK(hipMemcpyAsync(ho->logprobs, dl, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+    if (ho->flags) AXS_HIP_CHECK(hipMemcpyAsync(ho->flags, df, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+    if (ho->kept_ids)
+        AXS_HIP_CHECK(hipMemcpyAsync(ho->kept_ids, dk, (size_t)B * ho->kept_cap * 4, hipMemcpyDeviceToHost, s));
+    if (ho->kept_count) AXS_HIP_CHECK(hipMemcpyAsync(ho->kept_count, dc, (size_t)B * 4, hipMemcpyDeviceToHost, s));
+    if ((rc = order_end(ctx, s))) return rc;
+    AXS_HIP_CHECK(hipStreamSynchronize(s));
+    return AXS_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int sample_batch_locked(axs_context* ctx, const axs_batch_desc* d, const axs_outputs* o, hipStream_t s) {
     KArgs a{};
     a.logits = d->logits;
     a.logits2 = nullptr;
@@ -3755,6 +3982,7 @@ int axs_sample_batch(axs_context* ctx, const axs_batch_desc* d, const axs_output
     a.mtp_depth = 0;
     a.mtp_batch = 0;
     a.want_logprob = o->logprobs != nullptr;
+    a.exact_lp = 1;
     a.stride = d->row_stride;
     a.params = d->params;
     a.params2 = nullptr;
@@ -3780,6 +4008,10 @@ int axs_sample_batch(axs_context* ctx, const axs_batch_desc* d, const axs_output
     return run_pipeline(ctx, a, pl, s);
 }
 
+}  // namespace
+
+extern "C" {
+
 int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
                      int64_t row_stride, uint32_t* out_ids, float* out_logprob, void* stream) {
     if (!ctx || !logits || !out_ids) return fail(AXS_E_INVALID, "ctx, logits and out_ids must be non-NULL");
@@ -3787,6 +4019,7 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
     if (batch < 1 || vocab < 1 || row_stride < vocab) return fail(AXS_E_INVALID, "bad shape");
     if (batch > ctx->max_rows || vocab > ctx->max_vocab)
         return fail(AXS_E_CAPACITY, "batch or vocab larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
     DevGuard g(ctx->device);
     KArgs a{};
     a.logits = logits;
@@ -3803,9 +4036,10 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
     if (rc) return rc;
     fill_ws(a, ctx);
     hipStream_t s = (hipStream_t)stream;
+    if ((rc = order_begin(ctx, s))) return rc;
     timed(ctx, AXS_KERNEL_STREAM, s, [&] { launch_stream(pl, a, s); });
     AXS_HIP_CHECK(hipGetLastError());
-    return AXS_OK;
+    return order_end(ctx, s);
 }
 
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_outputs* o, void* stream) {
@@ -3819,8 +4053,11 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_output
     int64_t rows = (int64_t)d->batch * (2 * d->depth + 1);
     if (rows > ctx->max_rows || d->vocab > ctx->max_vocab)
         return fail(AXS_E_CAPACITY, "batch*(2*depth+1) rows or vocab larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
     DevGuard g(ctx->device);
     hipStream_t s = (hipStream_t)stream;
+    int rc0 = order_begin(ctx, s);
+    if (rc0) return rc0;
     KArgs a{};
     a.logits = d->target_logits;
     a.logits2 = d->draft_logits;
@@ -3845,11 +4082,12 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_output
                            o->out_ids, o->out_count, o->accept_count, o->flags);
     });
     AXS_HIP_CHECK(hipGetLastError());
-    return AXS_OK;
+    return order_end(ctx, s);
 }
 
 int axs_timing_enable(axs_context* ctx, int enable) {
     if (!ctx) return fail(AXS_E_INVALID, "ctx is NULL");
+    std::lock_guard<std::mutex> lk(ctx->mu);
     DevGuard g(ctx->device);
     clear_events(ctx);
     ctx->timing = enable != 0;
@@ -3859,6 +4097,7 @@ int axs_timing_enable(axs_context* ctx, int enable) {
 int axs_timing_read(axs_context* ctx, int kernel, double* total_ms, int* launches) {
     if (!ctx || !total_ms || !launches) return fail(AXS_E_INVALID, "NULL argument");
     if (kernel < 0 || kernel >= AXS_KERNEL_COUNT) return fail(AXS_E_INVALID, "bad kernel id");
+    std::lock_guard<std::mutex> lk(ctx->mu);
     DevGuard g(ctx->device);
     double t = 0.0;
     for (auto& e : ctx->ev[kernel]) {

@@ -19,8 +19,11 @@
  *     the null stream); all work is enqueued on it and the call returns
  *     without synchronising.
  *   - No torch or HIP types appear in the signatures.
- *   - Calls that share one context must not overlap (the context owns the
- *     device workspace); use one context per thread or serialise.
+ *   - A context may be shared by threads: its calls are serialised (a lock
+ *     around each call's enqueue), and a call on another stream than the
+ *     previous call's first waits for that call's work (an event), so the
+ *     context's workspace is never used by two streams at once.  One context
+ *     per thread avoids the waiting.
  */
 #ifndef AX_HIP_SAMPLER_H
 #define AX_HIP_SAMPLER_H
@@ -134,8 +137,10 @@ typedef struct axs_batch_desc {
 
 typedef struct axs_outputs {
     uint32_t* token_ids;   /* [batch], required                                   */
-    float*    logprobs;    /* [batch] or NULL: greedy rows -ln sum exp(l - max)
-                              (crates/ax-engine-core/src/sampling.rs:177-190);
+    float*    logprobs;    /* [batch] or NULL: greedy rows -ln sum exp(l - max),
+                              the sum taken as the core sampler takes it (f32,
+                              index order, reproduced bit for bit by the exact
+                              path: crates/ax-engine-core/src/sampling.rs:177-190);
                               sampled rows max(ln(p/F), -30)
                               (crates/ax-engine-mlx/src/sampling.rs:156-160)      */
     uint32_t* flags;       /* [batch] or NULL, AXS_FLAG_* bits                    */
@@ -207,6 +212,14 @@ int axs_abi_version(void);
 /* Thread-local message of the last failed call on this thread ("" if none). */
 const char* axs_last_error(void);
 
+/* Registers `handler`, called with the message of every failed call on the
+ * failing call's own thread, after axs_last_error() is set; NULL unregisters.
+ * The handler must not unwind into the library.  Mirrors the error-handler
+ * hook of crates/mlx-sys/native/ax_shim.h:106-110, which the reference
+ * records per thread on the Rust side (crates/mlx-sys/src/error.rs:21-99). */
+typedef void (*axs_error_handler_func)(const char* msg, void* data);
+void axs_set_error_handler(axs_error_handler_func handler, void* data);
+
 /* Creates a sampler context on `device` with device workspace sized for up to
  * max_batch rows of up to max_vocab entries (MTP counts depth*2+1 rows per
  * sequence).  Replaces the reference's per-request sampler buffers
@@ -219,13 +232,27 @@ int axs_context_destroy(axs_context* ctx);
 int axs_sample_batch(axs_context* ctx, const axs_batch_desc* desc,
                      const axs_outputs* out, void* stream);
 
+/* Batched sampling step over HOST arrays: the engine-level TokenSampler
+ * boundary (crates/ax-engine-core/src/sampling.rs:90-92), whose requests
+ * carry their logits as host vectors (SamplerRequest.logits, :78).  Same
+ * descriptor and outputs as axs_sample_batch, but EVERY pointer in `desc` and
+ * `out` is a host pointer: the library copies the inputs into device staging
+ * of the context (grown on demand) on the context's own stream, samples
+ * there, copies the outputs back and waits for them before returning.  Used
+ * by a HipTokenSampler implementation of the trait. */
+int axs_sample_batch_host(axs_context* ctx, const axs_batch_desc* desc, const axs_outputs* out);
+
 /* Greedy batched argmax + logprob over [batch, row_stride] logits: first
  * maximum (lowest id) wins, NaN skipped, all-NaN row -> 0
  * (crates/ax-engine-mlx/src/sampling.rs:954-966); replaces argmax_batched
  * (crates/ax-engine-mlx/src/batched_sampling.rs:102-111) and the Metal
  * sample_argmax_logprob_batched_f32 kernel
  * (metal/kernels/phase1_dense_path.metal:1273-1341).  out_logprob may be NULL;
- * it receives -ln sum_{finite l} exp(l - max) (NaN when the max is not finite). */
+ * it receives -ln sum_{finite l} exp(l - max) (NaN when the max is not finite),
+ * summed in a fixed order per row (bit-reproducible), within 1e-5 of the
+ * exact value; the core sampler's own f32 running sum, which drifts from it by
+ * up to ~1e-4 relative over 1e5 terms, is what axs_sample_batch returns for
+ * greedy rows. */
 int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
                      int vocab, int64_t row_stride, uint32_t* out_ids,
                      float* out_logprob, void* stream);

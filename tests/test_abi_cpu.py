@@ -68,3 +68,28 @@ def test_c_struct_sizes_from_the_compiler(tmp_path):
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     sizes = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
     assert sizes == ["64", "120", "48", "72", "32"]
+
+
+def test_error_handler_and_last_error_without_a_gpu():
+    """A call refused before any HIP call (bad sizes) sets the thread's last
+    error and calls the registered handler on this thread with the same
+    message; unregistering stops the calls."""
+    from ax_sampler import _abi
+
+    L = ctypes.CDLL(_abi.LIB_PATH)
+    L.axs_last_error.restype = ctypes.c_char_p
+    L.axs_context_create.restype = ctypes.c_int
+    L.axs_context_create.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.POINTER(ctypes.c_void_p)]
+    HANDLER = ctypes.CFUNCTYPE(None, ctypes.c_char_p, ctypes.c_void_p)
+    seen = []
+    h = HANDLER(lambda msg, data: seen.append((msg, data)))
+    L.axs_set_error_handler.argtypes = [HANDLER, ctypes.c_void_p]
+    L.axs_set_error_handler(h, ctypes.c_void_p(1234))
+    out = ctypes.c_void_p()
+    assert L.axs_context_create(0, 0, 10, ctypes.byref(out)) == 1  # AXS_E_INVALID
+    assert out.value is None
+    assert L.axs_last_error() == b"max_batch and max_vocab must be >= 1"
+    assert seen == [(b"max_batch and max_vocab must be >= 1", 1234)]
+    L.axs_set_error_handler(HANDLER(), None)
+    assert L.axs_context_create(0, 10, -1, ctypes.byref(out)) == 1
+    assert len(seen) == 1
