@@ -57,6 +57,7 @@ EXPORTS = (
     "axs_sample_batch",
     "axs_sample_batch_host",
     "axs_argmax_batch",
+    "axs_argmax_batch_noalloc",
     "axs_mtp_verify",
     "axs_timing_enable",
     "axs_timing_read",
@@ -178,6 +179,8 @@ def lib():
             L.axs_sample_batch_host.argtypes = [vp, C.POINTER(BatchDesc), C.POINTER(Outputs)]
             L.axs_argmax_batch.restype = i32
             L.axs_argmax_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp]
+            L.axs_argmax_batch_noalloc.restype = i32
+            L.axs_argmax_batch_noalloc.argtypes = [i32, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_mtp_verify.restype = i32
             L.axs_mtp_verify.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOutputs), vp]
             L.axs_timing_enable.restype = i32

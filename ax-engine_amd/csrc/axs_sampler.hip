@@ -3773,6 +3773,48 @@ int stage_at(axs_context* c, int i, size_t n, void** out) {
     return AXS_OK;
 }
 
+// ---------------------------------------------------------------------------
+// Scratch of axs_argmax_batch_noalloc: a file-scope device array instead of a
+// context.  The one-row (segmented) argmax publishes per-segment results
+// (ChunkStat), candidates (Cand) and an arrival counter there; batches of 2
+// rows or more (k_row) use none of it.  NA_SEGS segments cover the one-row
+// plan up to ROW_MAX ids (2,048-id segments).  Each GPU holds its own copy for
+// the life of the process; calls that overlap on one GPU race on it.
+// ---------------------------------------------------------------------------
+constexpr uint32_t NA_SEGS = 128;
+constexpr size_t NA_CSTAT_OFF = 0;
+constexpr size_t NA_POOL_OFF = NA_CSTAT_OFF + (size_t)NA_SEGS * sizeof(ChunkStat);
+constexpr size_t NA_DONE_OFF = NA_POOL_OFF + (size_t)NA_SEGS * CAPS * sizeof(Cand);
+constexpr size_t NA_DONE_WORDS = 2;  // row_done[0] and the (unused) exact-path counter
+constexpr size_t NA_SCRATCH_BYTES = NA_DONE_OFF + NA_DONE_WORDS * sizeof(uint32_t);
+static_assert(NA_POOL_OFF % 16 == 0 && NA_DONE_OFF % 16 == 0, "scratch carve-up alignment");
+
+static __device__ __align__(256) unsigned char scratch[NA_SCRATCH_BYTES];
+
+constexpr int NA_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NA_MAX_DEVICES];  // device address of `scratch` on each GPU
+
+// Device address of this GPU's `scratch` (device must be current); looked up
+// once per device.
+int scratch_ptr(int device, void** out) {
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[device]) {
+        void* ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(AXS_E_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_ptr[device] = ptr;
+    }
+    *out = g_scratch_ptr[device];
+    return AXS_OK;
+}
+
+__global__ void k_fill_u32(uint32_t* p, uint32_t n, uint32_t v) {
+    const uint32_t i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = v;
+}
+
 uint32_t next_pow2_h(uint32_t n) {
     uint32_t p = 1;
     while (p < n) p <<= 1;
@@ -4040,6 +4082,48 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
     timed(ctx, AXS_KERNEL_STREAM, s, [&] { launch_stream(pl, a, s); });
     AXS_HIP_CHECK(hipGetLastError());
     return order_end(ctx, s);
+}
+
+int axs_argmax_batch_noalloc(int device, const void* logits, int dtype, int batch, int vocab,
+                             int64_t row_stride, uint32_t* out_ids, float* out_logprob, void* stream) {
+    if (!logits || !out_ids) return fail(AXS_E_INVALID, "logits and out_ids must be non-NULL");
+    if (dtype != AXS_DTYPE_F32 && dtype != AXS_DTYPE_BF16) return fail(AXS_E_INVALID, "bad dtype");
+    if (batch < 1 || vocab < 1 || row_stride < vocab) return fail(AXS_E_INVALID, "bad shape");
+    if ((uint32_t)vocab > ROW_MAX)
+        return fail(AXS_E_CAPACITY, "axs_argmax_batch_noalloc: vocab above 262144 (its scratch limit)");
+    int ndev = 0;
+    if (hipGetDeviceCount(&ndev) != hipSuccess || device < 0 || device >= ndev || device >= NA_MAX_DEVICES)
+        return fail(AXS_E_INVALID, "no such HIP device");
+    DevGuard g(device);
+    KArgs a{};
+    a.logits = logits;
+    a.dtype = dtype;
+    a.nrows = batch;
+    a.vocab = vocab;
+    a.stride = row_stride;
+    a.params = nullptr;
+    a.want_logprob = out_logprob != nullptr;
+    a.out_ids = out_ids;
+    a.out_lp = out_logprob;
+    Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
+    if (!pl.wide && (int64_t)batch * pl.snch > (int64_t)NA_SEGS)
+        return fail(AXS_E_CAPACITY, "axs_argmax_batch_noalloc: more segments than its scratch holds (128)");
+    int rc = apply_plan(a, pl);
+    if (rc) return rc;
+    void* base = nullptr;
+    if ((rc = scratch_ptr(device, &base))) return rc;
+    char* sp = (char*)base;
+    a.cstat = (ChunkStat*)(sp + NA_CSTAT_OFF);
+    a.pool = (Cand*)(sp + NA_POOL_OFF);
+    a.row_done = (uint32_t*)(sp + NA_DONE_OFF);
+    a.ex_done = a.row_done + 1;
+    hipStream_t s = (hipStream_t)stream;
+    // the arrival counters start at zero (a fill kernel, not a memset node,
+    // so that the call can be captured in a graph)
+    hipLaunchKernelGGL(k_fill_u32, dim3(1), dim3(64), 0, s, a.row_done, (uint32_t)NA_DONE_WORDS, 0u);
+    launch_stream(pl, a, s);
+    AXS_HIP_CHECK(hipGetLastError());
+    return AXS_OK;
 }
 
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_outputs* o, void* stream) {

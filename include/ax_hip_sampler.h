@@ -257,6 +257,22 @@ int axs_argmax_batch(axs_context* ctx, const void* logits, int dtype, int batch,
                      int vocab, int64_t row_stride, uint32_t* out_ids,
                      float* out_logprob, void* stream);
 
+/* Greedy batched argmax + logprob with the result of axs_argmax_batch, but no
+ * context and no device allocation.  No counterpart in the reference: it is
+ * for callers that cannot allocate (code under HIP graph capture, serving
+ * loops or harnesses that forbid hipMalloc).  Its scratch (per-segment
+ * results of the one-row shape, ~260 KB) is a static device array of the
+ * library, one per GPU for the life of the process, looked up on the first
+ * call on `device`; each call clears what must start at zero with a fill
+ * kernel on `stream`.  Limits: vocab <= 262144 and at most 128 scratch
+ * segments (a one-row call up to 262,144 ids uses at most 128; batches of 2
+ * rows or more use none); beyond them AXS_E_CAPACITY.  Calls that overlap on
+ * one GPU (on different streams or threads) race on the shared scratch:
+ * serialise them. */
+int axs_argmax_batch_noalloc(int device, const void* logits, int dtype, int batch, int vocab,
+                             int64_t row_stride, uint32_t* out_ids, float* out_logprob,
+                             void* stream);
+
 /* MTP speculative verify (see axs_mtp_desc). */
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
                    const axs_mtp_outputs* out, void* stream);
