@@ -29,6 +29,7 @@ FLAG_NEAR_NUCLEUS = 1 << 5
 FLAG_NEAR_MINP = 1 << 6
 FLAG_NEAR_TIE = 1 << 7
 FLAG_NEAR_ANY = FLAG_NEAR_DRAW | FLAG_NEAR_NUCLEUS | FLAG_NEAR_MINP | FLAG_NEAR_TIE
+FLAG_CAPACITY = 1 << 8
 FLAG_ERROR = 1 << 31
 
 MTP_FLAG_RESIDUAL = 1 << 0

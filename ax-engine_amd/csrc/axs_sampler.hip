@@ -73,6 +73,7 @@ constexpr float P_FLOOR = 0x1p-24f;   // smaller terms never change a sum >= 1
 // chunk-stat flags
 constexpr uint32_t CS_OVERFLOW = 1u;
 constexpr uint32_t CS_ERROR = 2u;
+constexpr uint32_t CS_CAPACITY = 4u;  // with CS_ERROR: more bias entries than the kernel holds
 
 // A segment's result, published as two 64-bit words (see pub_u64)
 struct ChunkStat {
@@ -283,7 +284,9 @@ struct ProcLds {
     static constexpr uint32_t NW = SEGMAX / 32;      // bitmap words
     static constexpr uint32_t PW = NW / NT;          // bitmap words per thread
     static constexpr uint32_t RCAP = NT >= 1024 ? SEGMAX / 32 : SEGMAX / 64;  // ranked special ids
-    static constexpr uint32_t BCAP = NT >= 1024 ? 1024u : BIAS_LDS;  // bias entries
+    // bias entries per segment: the exact-path segments hold as many as a
+    // k_row row (RBCAP), so no row that k_row accepted overflows them
+    static constexpr uint32_t BCAP = (NT >= 1024 || SEGMAX == EX_SEGMAX) ? 1024u : BIAS_LDS;
     uint32_t spec[NW];
     uint16_t pre[NW];
     uint32_t sid[RCAP];
@@ -978,7 +981,7 @@ __device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_s
     }
     if (fl & CS_ERROR) {
         if (tid == 0) {
-            write_row(a, r, 0u, NAN, AXS_FLAG_ERROR);
+            write_row(a, r, 0u, NAN, AXS_FLAG_ERROR | ((fl & CS_CAPACITY) ? AXS_FLAG_CAPACITY : 0u));
             if (a.out_kept_count) a.out_kept_count[r] = 0;
             if (a.ws_kept_id) {
                 a.rstate[r].kept = 0;
@@ -1421,7 +1424,7 @@ __global__ __launch_bounds__(NT) void k_stream(KArgs a) {
     // path for it need none)
     const bool gsum_on = mode == M_GREEDY && a.want_logprob && !a.exact_lp;
     const float thr = gather ? __fsub_rn(ln_f32(c.p.min_p), 1e-3f) : 0.0f;
-    const uint32_t sflags = (c.err || (c.any_proc && L.err)) ? CS_ERROR : 0u;
+    const uint32_t sflags = c.err ? CS_ERROR : ((c.any_proc && L.err) ? (CS_ERROR | CS_CAPACITY) : 0u);
 
     float tm = -INFINITY;             // thread maximum (non-special ids)
     uint32_t ta = NONE;               // its lowest id
@@ -2064,7 +2067,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     // path for it need none)
     const bool gsum_on = mode == M_GREEDY && a.want_logprob && !a.exact_lp;
     const float thr = gather ? __fsub_rn(ln_f32(c.p.min_p), 1e-3f) : 0.0f;
-    const uint32_t sflags = (c.err || (SL.err & RERR_BIAS)) ? CS_ERROR : 0u;
+    const uint32_t sflags = c.err ? CS_ERROR : ((SL.err & RERR_BIAS) ? (CS_ERROR | CS_CAPACITY) : 0u);
     // Processors that can only lower a logit (repetition >= 1, presence and
     // frequency >= 0, biases <= 0, mask, ban) let the stream skip every
     // vector whose raw maximum is below rthr: none of its plain elements can
@@ -3019,12 +3022,18 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
 
     // index-order rows: the kept-set size and the ordered kept lists, by the
     // whole block
-    uint32_t dkept = 0, dlist = 0;
+    uint32_t dkept = 0, dlist = 0, dpos = 0;
     if (!sorted) {
         const bool mp = rs.mode == M_MINP;
-        uint32_t cnt = 0;
-        for (uint32_t i = tid; i < V; i += NT_EX) cnt += (!mp || dense[i] > 0.0f) ? 1u : 0u;
+        uint32_t cnt = 0, cpos = 0;
+        for (uint32_t i = tid; i < V; i += NT_EX) {
+            cnt += (!mp || dense[i] > 0.0f) ? 1u : 0u;
+            cpos += dense[i] > 0.0f ? 1u : 0u;
+        }
         dkept = block_sum_u32<NT_EX>(cnt, s_u);
+        // the distribution's entries (TokenDistribution::new keeps p > 0,
+        // crates/ax-engine-mlx/src/sampling.rs:128-144)
+        if (a.ws_kept_id) dpos = block_sum_u32<NT_EX>(cpos, s_u);
         // out_kept: ids with (!min-p || p > 0); ws lists: ids with p > 0
         const uint32_t cap_o = (a.out_kept && a.out_kept_cap > 0) ? (uint32_t)a.out_kept_cap : 0u;
         const uint32_t cap_w = a.ws_kept_id ? KEPT_CAP : 0u;
@@ -3173,6 +3182,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             if (kept > Lk) flags |= AXS_FLAG_ERROR;
         } else {
             o = dlist;
+            kept = dpos;  // an MTP distribution counts its p > 0 entries
         }
         if (kept > KEPT_CAP) flags |= AXS_FLAG_ERROR;
         a.rstate[r].kept = kept;
@@ -3965,6 +3975,11 @@ int axs_sample_batch_host(axs_context* ctx, const axs_batch_desc* hd, const axs_
     if (hd->mask_words) {
         if ((rc = up(4, hd->mask_words, (size_t)B * hd->mask_stride * 4, &p))) return rc;
         d.mask_words = (const uint32_t*)p;
+    }
+    if (hd->bias_ids && B >= 2) {
+        for (int r = 0; r < B; ++r)
+            if (hd->bias_offsets[r + 1] - hd->bias_offsets[r] > (int64_t)RBCAP)
+                return fail(AXS_E_CAPACITY, "a row has more than 1024 bias entries (AXS_BIAS_ROW_MAX)");
     }
     if (hd->bias_ids) {
         if ((rc = up(5, hd->bias_ids, (size_t)hd->bias_len * 4, &p))) return rc;

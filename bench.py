@@ -14,10 +14,16 @@ Prints one JSON line:
   value         rows/s of the whole step (all kernels, hipEvents on the
                 launch stream, K timed steps)
   roofline      the dominant kernel: its algorithmic bytes per launch / its
-                average duration from hipEvents on its launch stream;
-                ``traffic`` = HBM bytes per launch measured by rocprofv3
-                (FETCH_SIZE + WRITE_SIZE, copy-calibrated) from the committed
-                profile summary, when there is one for this config
+                average duration.  When the step is that one kernel (C2,
+                C3, C4: k_row decides every row in place), the duration is
+                the step time of back-to-back launches (hipEvents on the
+                launch stream around K steps) if that is below the
+                hipEvent-bracketed time of single launches; otherwise the
+                latter (``kernel_timing`` says which).  ``traffic`` = HBM
+                bytes per launch of that kernel measured by rocprofv3
+                (FETCH_SIZE + WRITE_SIZE, copy-calibrated) and
+                ``rocprof_avg_us`` its kernel-trace average, both from the
+                committed profile summary of this config
   cpu_baseline  the CPU restatement of the reference sampler (oracle/, the
                 reference's own Rust cannot be built here) on a bounded sample
                 of the same rows, timed on this host
@@ -55,19 +61,23 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
-def measured_traffic(cfg):
-    """HBM bytes per launch of the dominant kernel on this config, from the
-    committed rocprofv3 summary (copy-calibrated FETCH_SIZE + WRITE_SIZE); None
-    if there is none."""
-    path = os.path.join(ROOT, "profiles", f"k_row_{cfg.lower()}.md" if cfg == "C3" else f"{cfg.lower()}.md")
-    try:
+def profile_figures(cfg):
+    """Figures of the committed rocprofv3 summary for this config
+    (profiles/*_<cfg>.md): `traffic_bytes_per_launch=` (copy-calibrated
+    FETCH_SIZE + WRITE_SIZE of the dominant kernel) and `rocprof_avg_us=`
+    (its kernel-trace average).  Missing figures are None."""
+    import glob
+
+    out = {"traffic": None, "rocprof_avg_us": None, "file": None}
+    for path in sorted(glob.glob(os.path.join(ROOT, "profiles", f"*_{cfg.lower()}.md"))):
         with open(path) as f:
             for line in f:
-                if line.startswith("traffic_bytes_per_launch"):
-                    return int(line.split("=")[1])
-    except OSError:
-        pass
-    return None
+                if line.startswith("traffic_bytes_per_launch="):
+                    out["traffic"] = int(line.split("=")[1])
+                    out["file"] = os.path.relpath(path, ROOT)
+                elif line.startswith("rocprof_avg_us="):
+                    out["rocprof_avg_us"] = float(line.split("=")[1])
+    return out
 
 
 def cpu_rows_per_s(fn, rows_per_call, seconds=12.0, max_threads=16):
@@ -258,6 +268,17 @@ def main():
     kern = {(name0 if k == "k_stream" else k): v for k, v in kern.items()}
     dom = max(kern.items(), key=lambda kv: kv[1]["avg_us"])
     dom_name, dom_us = dom[0], dom[1]["avg_us"]
+    # One launch per step: the step time of K back-to-back launches is the
+    # kernel's own time plus the gap between launches, and never more than
+    # the event-bracketed time of a single launch (which adds the events'
+    # latency); the roofline uses the smaller.  Several kernels per step:
+    # the dominant one's event-bracketed average.
+    single = len(kern) == 1 and dom[1]["launches"] == args.steps
+    timing_src = "hipEvents around each launch"
+    if single and ms_step * 1e3 < dom_us:
+        dom_us = ms_step * 1e3
+        timing_src = "step time (one launch per step, back to back)"
+    prof = profile_figures(cfg)
     if dom_name in ("k_row", "k_stream"):
         dom_alg = alg
     elif dom_name == "k_exact_mat":
@@ -307,10 +328,13 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4) if achieved else None,
-            "traffic": measured_traffic(cfg) if dom_name in ("k_row", "k_stream") else None,
-            "traffic_source": "profiles/ (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE; scaled by a 256 MiB copy's readings)",
+            "traffic": prof["traffic"],
+            "traffic_source": (f"{prof['file']} (rocprofv3 --pmc FETCH_SIZE, WRITE_SIZE of {dom_name}; "
+                               "scaled by a 256 MiB copy's readings)") if prof["file"] else None,
             "algorithmic_bytes": dom_alg,
             "kernel_avg_us": round(dom_us, 3),
+            "kernel_timing": timing_src,
+            "rocprof_avg_us": prof["rocprof_avg_us"],
             "step_GBps": round(alg / (ms_step * 1e-3) / 1e9, 1),
         },
         "kernels": {k: {"avg_us": round(v["avg_us"], 3), "launches": v["launches"]} for k, v in kern.items()},

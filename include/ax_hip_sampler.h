@@ -133,7 +133,22 @@ typedef struct axs_batch_desc {
 #define AXS_FLAG_NEAR_NUCLEUS    (1u << 5)  /* |cum - top_p*total| < 1e-6 total  */
 #define AXS_FLAG_NEAR_MINP       (1u << 6)  /* |p - min_p| < 1e-6 min_p          */
 #define AXS_FLAG_NEAR_TIE        (1u << 7)  /* p within 2 ulp across the top-k cut */
-#define AXS_FLAG_ERROR           (1u << 31) /* invalid row input (token 0)       */
+#define AXS_FLAG_CAPACITY        (1u << 8)  /* with AXS_FLAG_ERROR: the row has more
+                                               bias entries than the kernel holds
+                                               (AXS_BIAS_ROW_MAX / AXS_BIAS_SEG_MAX) */
+#define AXS_FLAG_ERROR           (1u << 31) /* invalid row input, or a capacity
+                                               refusal (AXS_FLAG_CAPACITY): token 0 */
+
+/* Logit-bias capacity.  Batches of 2 rows or more: up to AXS_BIAS_ROW_MAX
+ * entries per row.  A batch of one row is cut into segments of at most
+ * 65,536 ids, each holding up to AXS_BIAS_SEG_MAX entries: any row of up to
+ * AXS_BIAS_SEG_MAX entries is accepted, a longer one when its entries spread
+ * over the segments.  A row beyond these gets token 0 with AXS_FLAG_ERROR |
+ * AXS_FLAG_CAPACITY (AXS_OK is still returned: the other rows are valid);
+ * axs_sample_batch_host, which sees the offsets, returns AXS_E_CAPACITY for a
+ * batch of 2 rows or more with a row above AXS_BIAS_ROW_MAX. */
+#define AXS_BIAS_ROW_MAX 1024
+#define AXS_BIAS_SEG_MAX 256
 
 typedef struct axs_outputs {
     uint32_t* token_ids;   /* [batch], required                                   */

@@ -178,3 +178,24 @@ def test_kept_set_beyond_capacity_declines(sampler, oracle):
     g_ids = res.out_ids.cpu().numpy().view(np.uint32)
     for b in (1, 3):
         assert n[b] == c_n[b] and np.array_equal(g_ids[b, :n[b]], c_ids[b, :c_n[b]])
+
+
+def test_index_order_laws_with_zero_probabilities(sampler, oracle):
+    """No top-k / top-p / min-p: the distribution is every id with p > 0 in
+    index order (TokenDistribution::new drops p = 0,
+    crates/ax-engine-mlx/src/sampling.rs:128-144).  Rows with -inf logits
+    (p = 0) are held to the oracle, not declined."""
+    rng = np.random.default_rng(88)
+    B, D, V = 6, 2, 1500
+    t = rng.standard_normal((B, D + 1, V), dtype=np.float32) * np.float32(2.0)
+    d = t[:, :D, :] + rng.standard_normal((B, D, V), dtype=np.float32) * np.float32(0.4)
+    t[:, :, rng.integers(0, V, 40)] = -np.inf
+    d[:, :, rng.integers(0, V, 40)] = -np.inf
+    _, _, tp, dp = make_c5(47, B=B, depth=D, V=16)
+    tp["temperature"], tp["top_p"], tp["top_k"] = 1.0, 1.0, 0
+    dp["temperature"], dp["top_p"], dp["top_k"] = 1.0, 1.0, 0
+    tp["has_min_p"] = 0
+    dp["has_min_p"] = 0
+    dids = _draft_ids(oracle, d, DTYPE_F32, B, D, V, dp, 61)
+    us = rng.random((B, D + 1)).astype(np.float32)
+    _run(sampler, oracle, t, d, DTYPE_F32, tp, dp, dids, us, "index-order with p = 0")

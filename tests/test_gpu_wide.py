@@ -146,3 +146,36 @@ def test_capture_pool_overflow(sampler, oracle, B):
     gpu = run_gpu(sampler, w, us, kept_cap=16)
     cpu = run_oracle(oracle, w, us, kept_cap=16)
     log(f"capture pool overflow, B={B}: {compare(w, gpu, cpu, f'capture-overflow-{B}')}")
+
+
+def test_bias_capacity_is_flagged_not_wrong(sampler, oracle):
+    """A row with more bias entries than the kernel holds (1024 per row from
+    2 rows on) comes back as token 0 with AXS_FLAG_ERROR | AXS_FLAG_CAPACITY;
+    the other rows are sampled as usual, and the host entry point refuses
+    the batch with AXS_E_CAPACITY."""
+    from ax_sampler import _abi
+    from ax_sampler.synth import make_mixed
+
+    w = make_mixed(71, 4, 8192, DTYPE_F32, hist_len=64, mask=False, bias=True, ngram=False)
+    rs = np.random.default_rng(72)
+    rows = [(w.bias_ids[w.bias_off[r]:w.bias_off[r + 1]], w.bias_vals[w.bias_off[r]:w.bias_off[r + 1]])
+            for r in range(w.B)]
+    rows[1] = (rs.integers(0, 8192, 1025).astype(np.uint32), rs.uniform(-1, 1, 1025).astype(np.float32))
+    us = _uniforms(w.B, 73)
+    from gpu_common import hist_rows, to_device
+    import torch
+
+    res = sampler.sample(to_device(w), w.params, history=hist_rows(w), bias=rows, uniforms=us, logprobs=True)
+    torch.cuda.synchronize()
+    tid, _, fl, _, _ = res.numpy()
+    assert fl[1] & np.uint32(_abi.FLAG_ERROR) and fl[1] & np.uint32(_abi.FLAG_CAPACITY) and tid[1] == 0
+    ids = np.concatenate([r[0] for r in rows]).astype(np.uint32)
+    vals = np.concatenate([r[1] for r in rows]).astype(np.float32)
+    off = np.zeros(w.B + 1, np.int64)
+    off[1:] = np.cumsum([len(r[0]) for r in rows])
+    want, ex, _ = oracle.sample_batch(w.logits, w.dtype, w.B, w.V, w.V, w.params, w.hist, w.hist_off,
+                                      None, 0, ids, vals, off, us)
+    for r in (0, 2, 3):
+        assert not fl[r] & np.uint32(_abi.FLAG_ERROR) and tid[r] == want[r], r
+    with pytest.raises(_abi.SamplerError, match="1024 bias entries"):
+        sampler.sample_host(w.logits, w.params, history=hist_rows(w), bias=rows, uniforms=us)
