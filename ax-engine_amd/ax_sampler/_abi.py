@@ -60,6 +60,7 @@ EXPORTS = (
     "axs_argmax_batch",
     "axs_argmax_batch_noalloc",
     "axs_mtp_verify",
+    "axs_token_logprob_batch",
     "axs_timing_enable",
     "axs_timing_read",
 )
@@ -182,6 +183,8 @@ def lib():
             L.axs_argmax_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_argmax_batch_noalloc.restype = i32
             L.axs_argmax_batch_noalloc.argtypes = [i32, vp, i32, i32, i32, i64, vp, vp, vp]
+            L.axs_token_logprob_batch.restype = i32
+            L.axs_token_logprob_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
             L.axs_mtp_verify.restype = i32
             L.axs_mtp_verify.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOutputs), vp]
             L.axs_timing_enable.restype = i32

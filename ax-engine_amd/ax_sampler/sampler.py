@@ -348,6 +348,23 @@ class HipSampler:
                                            self._stream(stream)))
         return ids, lp
 
+    def token_logprob(self, logits, tokens, temperatures, stream=None):
+        """full_vocab_token_logprob per row (axs_token_logprob_batch):
+        max(ln softmax(l / T)[t], -30) over device logits [B, V]."""
+        torch = _torch()
+        if logits.stride(1) != 1:
+            logits = logits.contiguous()
+        B, V = logits.shape
+        tok = tokens if isinstance(tokens, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(np.asarray(tokens, dtype=np.uint32)).view(np.int32)).to(self.device)
+        tem = temperatures if isinstance(temperatures, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(np.asarray(temperatures, dtype=np.float32))).to(self.device)
+        out = torch.empty(B, dtype=torch.float32, device=self.device)
+        _abi.check(self.L.axs_token_logprob_batch(self.ctx, logits.data_ptr(), _dtype_code(logits), B, V,
+                                                  logits.stride(0), tok.data_ptr(), tem.data_ptr(),
+                                                  out.data_ptr(), self._stream(stream)))
+        return out
+
     def mtp_verify(self, target, draft, draft_ids, target_params, draft_params, uniforms=None,
                    stream=None) -> MtpResult:
         """target [B, D+1, V], draft [B, D, V] on device; draft_ids [B, D]."""

@@ -172,6 +172,10 @@ struct KArgs {
     int32_t inplace;      // k_row: a row's exact path in its own workgroup (else listed)
     int32_t exact_lp;     // greedy rows' logprob: the core sampler's sequential sum (exact path)
     int32_t pad0;
+    // full-vocabulary token logprob rows (axs_token_logprob_batch): the token
+    // and temperature of each row; the row's law is the untruncated softmax
+    const uint32_t* lp_tokens;
+    const float* lp_temps;
     int64_t stride;
     const axs_sampling_params* params;
     const axs_sampling_params* params2;
@@ -226,9 +230,9 @@ __device__ __forceinline__ const char* row_ptr(const KArgs& a, int r) {
 }
 
 __device__ __forceinline__ axs_sampling_params row_params(const KArgs& a, int r) {
-    if (a.params == nullptr) {  // plain argmax entry point
+    if (a.params == nullptr) {  // plain argmax entry point, or a token-logprob row
         axs_sampling_params p;
-        p.temperature = 0.0f;
+        p.temperature = a.lp_temps ? a.lp_temps[r] : 0.0f;
         p.top_p = 1.0f;
         p.top_k = 0;
         p.min_p = 0.0f;
@@ -989,6 +993,30 @@ __device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_s
                 a.rstate[r].flags = AXS_FLAG_ERROR;
             }
         }
+        return false;
+    }
+    if (a.lp_tokens) {
+        // full_vocab_token_logprob (crates/ax-engine-mlx/src/sampling.rs:761-787):
+        // t >= V -> -30; T <= 0 -> 0 for the first maximum, else -inf; no
+        // finite maximum -> every term NaN -> zero sum -> -30; otherwise the
+        // exact path's index-order normaliser at T
+        const uint32_t t = a.lp_tokens[r];
+        const bool direct = t >= (uint32_t)a.vocab || mode == M_GREEDY || !isfinite(m) ||
+                            !isfinite(__fdiv_rn(1.0f, p.temperature));
+        if (direct) {
+            if (tid == 0) {
+                float lp = -30.0f;
+                if (t < (uint32_t)a.vocab && mode == M_GREEDY) lp = am == t ? 0.0f : -INFINITY;
+                write_row(a, r, t, lp, AXS_FLAG_EXACT_PATH);
+            }
+            return false;
+        }
+        const float inv = __fdiv_rn(1.0f, p.temperature);
+        if (INPLACE) {
+            *xs = exact_state(a, r, p, m, inv, M_FAST, false, am);
+            return true;
+        }
+        if (tid == 0) list_exact(a, r, p, m, inv, M_FAST, false, am);
         return false;
     }
     if (mode == M_GREEDY) {
@@ -3005,6 +3033,18 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     __threadfence_block();
     __syncthreads();  // every S store complete before the decisions read S
 
+    if (a.lp_tokens) {
+        // token-logprob row: max(ln(max(p_t / S, 1e-37)), -30) with S the
+        // index-order f32 sum (crates/ax-engine-mlx/src/sampling.rs:772-786)
+        if (tid == 0) {
+            const uint32_t t = a.lp_tokens[r];
+            const float F0 = S[V - 1];
+            float lp = -30.0f;
+            if (F0 > 0.0f && isfinite(F0)) lp = logprob_of(__fdiv_rn(dense[t], F0));
+            write_row(a, r, t, lp, AXS_FLAG_EXACT_PATH);
+        }
+        return;
+    }
     if (rs.mode == M_GREEDY) {
         // greedy row listed for its logprob: -ln of the index-order sum
         // (crates/ax-engine-core/src/sampling.rs:179-190); the token is the
@@ -4139,6 +4179,36 @@ int axs_argmax_batch_noalloc(int device, const void* logits, int dtype, int batc
     launch_stream(pl, a, s);
     AXS_HIP_CHECK(hipGetLastError());
     return AXS_OK;
+}
+
+int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
+                            int64_t row_stride, const uint32_t* tokens, const float* temperatures,
+                            float* out_logprob, void* stream) {
+    if (!ctx || !logits || !tokens || !temperatures || !out_logprob)
+        return fail(AXS_E_INVALID, "ctx, logits, tokens, temperatures and out_logprob must be non-NULL");
+    if (dtype != AXS_DTYPE_F32 && dtype != AXS_DTYPE_BF16) return fail(AXS_E_INVALID, "bad dtype");
+    if (batch < 1 || vocab < 1 || row_stride < vocab) return fail(AXS_E_INVALID, "bad shape");
+    if (batch > ctx->max_rows || vocab > ctx->max_vocab)
+        return fail(AXS_E_CAPACITY, "batch or vocab larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DevGuard g(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = order_begin(ctx, s);
+    if (rc) return rc;
+    KArgs a{};
+    a.logits = logits;
+    a.dtype = dtype;
+    a.nrows = batch;
+    a.vocab = vocab;
+    a.stride = row_stride;
+    a.params = nullptr;
+    a.lp_tokens = tokens;
+    a.lp_temps = temperatures;
+    a.out_ids = ctx->mtp_tok;  // the rows' tokens echoed: scratch
+    a.out_lp = out_logprob;
+    Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
+    if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
+    return order_end(ctx, s);
 }
 
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_outputs* o, void* stream) {

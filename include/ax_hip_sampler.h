@@ -288,6 +288,19 @@ int axs_argmax_batch_noalloc(int device, const void* logits, int dtype, int batc
                              int64_t row_stride, uint32_t* out_ids, float* out_logprob,
                              void* stream);
 
+/* Full-vocabulary log-probability of one token per row:
+ *   max(ln(max(softmax(l / T)[t], 1e-37)), -30)
+ * over [batch, row_stride] logits, the softmax's normaliser summed as the
+ * reference sums it (f32, index order, non-finite terms 0); T <= 0 gives 0
+ * for the first maximum and -inf otherwise, t >= vocab gives -30.
+ * full_vocab_token_logprob (crates/ax-engine-mlx/src/sampling.rs:761-787) per
+ * row, e.g. the draft log-prob of MTP rejection sampling in the
+ * full-softmax domain (crates/ax-engine-mlx/src/mtp.rs:203-220).  tokens
+ * [batch], temperatures [batch] and out_logprob [batch] are device arrays. */
+int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
+                            int64_t row_stride, const uint32_t* tokens, const float* temperatures,
+                            float* out_logprob, void* stream);
+
 /* MTP speculative verify (see axs_mtp_desc). */
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
                    const axs_mtp_outputs* out, void* stream);

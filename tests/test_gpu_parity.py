@@ -182,3 +182,43 @@ def test_greedy_logprob_is_the_core_sum(sampler, oracle, dtype, B, V):
         worst = max(worst, abs(float(lp[r]) - core[1]) / ulp)
         assert abs(float(lp[r]) - core[1]) <= ulp, (r, float(lp[r]), core[1])
     log(f"greedy logprob dtype={dtype} B={B} V={V}: worst {worst:.2f} ulp of the core value")
+
+
+@pytest.mark.parametrize("dtype,B,V", [(DTYPE_F32, 1, 151936), (DTYPE_BF16, 24, 151936), (DTYPE_F32, 80, 4099)])
+def test_token_logprob_matches_full_vocab_token_logprob(sampler, oracle, dtype, B, V):
+    """axs_token_logprob_batch against the oracle's full_vocab_token_logprob
+    (crates/ax-engine-mlx/src/sampling.rs:761-787): the normaliser is the
+    reference's index-order f32 sum reproduced bit for bit, so values agree
+    to the last ulp of ln.  Covers the argmax, a random and the least likely
+    token, T <= 0, an out-of-range id, an all -inf row and a NaN token."""
+    import torch
+
+    rs = np.random.default_rng([7, B, V])
+    x = (rs.standard_normal((B, V), dtype=np.float32) * np.float32(3.0))
+    temps = rs.choice(np.array([0.6, 1.0, 1.7], np.float32), B)
+    toks = rs.integers(0, V, B).astype(np.uint32)
+    if B > 3:
+        x[1, :] = -np.inf
+        x[2, toks[2]] = np.nan
+        temps[3] = 0.0
+        toks[0] = V + 5
+    for r in range(4, B, 3):
+        toks[r] = int(np.argmax(x[r]))
+    if dtype == DTYPE_BF16:
+        bits = f32_to_bf16_bits(x)
+        xf = oracle.bf16_to_f32(bits)
+        t = torch.from_numpy(bits.view(np.int16)).view(torch.bfloat16).cuda()
+    else:
+        xf = x
+        t = torch.from_numpy(x).cuda()
+    got = sampler.token_logprob(t, toks, temps).cpu().numpy()
+    worst = 0.0
+    for r in range(B):
+        want = oracle.full_vocab_token_logprob(xf[r], int(toks[r]), float(temps[r]))
+        if math.isinf(want):
+            assert got[r] == want, (r, got[r], want)
+            continue
+        ulp = float(np.spacing(np.float32(abs(want))))
+        worst = max(worst, abs(float(got[r]) - want) / ulp)
+        assert abs(float(got[r]) - want) <= ulp, (r, float(got[r]), want)
+    log(f"token logprob dtype={dtype} B={B} V={V}: worst {worst:.2f} ulp")
