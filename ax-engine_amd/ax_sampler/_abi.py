@@ -36,7 +36,14 @@ MTP_FLAG_RESIDUAL = 1 << 0
 MTP_FLAG_BONUS = 1 << 1
 MTP_FLAG_NEAR_ACCEPT = 1 << 2
 MTP_FLAG_NEAR = 1 << 3
+MTP_FLAG_CORRECTION = 1 << 4
+MTP_FLAG_TAIL_ROW = 1 << 5
 MTP_FLAG_ERROR = 1 << 31
+
+MTP_SRC_DEFAULT, MTP_SRC_MTP, MTP_SRC_GEMMA, MTP_SRC_NGRAM, MTP_SRC_HYBRID = range(5)
+MTP_MODEL_GREEDY, MTP_MODEL_REJECTION = 0, 1
+MTP_NGRAM_CONFIDENCE, MTP_NGRAM_DELTA, MTP_NGRAM_GREEDY = 0, 1, 2
+MTP_LNQ_DISTRIBUTION, MTP_LNQ_FULL_SOFTMAX = 0, 1
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -60,6 +67,7 @@ EXPORTS = (
     "axs_argmax_batch",
     "axs_argmax_batch_noalloc",
     "axs_mtp_verify",
+    "axs_mtp_verify_ex",
     "axs_token_logprob_batch",
     "axs_timing_enable",
     "axs_timing_read",
@@ -133,6 +141,18 @@ class MtpDesc(C.Structure):
     ]
 
 
+class MtpOptions(C.Structure):
+    _fields_ = [
+        ("sources", C.c_void_p),
+        ("pending_log_probs", C.c_void_p),
+        ("predicted", C.c_void_p),
+        ("model_mode", C.c_int32),
+        ("ngram_mode", C.c_int32),
+        ("lnq_mode", C.c_int32),
+        ("delta_correction", C.c_int32),
+    ]
+
+
 class MtpOutputs(C.Structure):
     _fields_ = [
         ("out_ids", C.c_void_p),
@@ -185,6 +205,8 @@ def lib():
             L.axs_argmax_batch_noalloc.argtypes = [i32, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_token_logprob_batch.restype = i32
             L.axs_token_logprob_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
+            L.axs_mtp_verify_ex.restype = i32
+            L.axs_mtp_verify_ex.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOptions), C.POINTER(MtpOutputs), vp]
             L.axs_mtp_verify.restype = i32
             L.axs_mtp_verify.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOutputs), vp]
             L.axs_timing_enable.restype = i32

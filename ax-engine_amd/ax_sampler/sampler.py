@@ -366,8 +366,12 @@ class HipSampler:
         return out
 
     def mtp_verify(self, target, draft, draft_ids, target_params, draft_params, uniforms=None,
-                   stream=None) -> MtpResult:
-        """target [B, D+1, V], draft [B, D, V] on device; draft_ids [B, D]."""
+                   stream=None, options: Optional[dict] = None) -> MtpResult:
+        """target [B, D+1, V], draft [B, D, V] on device; draft_ids [B, D].
+        ``options`` (dict) selects ``axs_mtp_verify_ex``: ``sources`` /
+        ``pending_log_probs`` / ``predicted`` ([B, D] arrays or None),
+        ``model_mode``, ``ngram_mode``, ``lnq_mode``, ``delta_correction``;
+        its uniforms are taken in the reference's stream order."""
         torch = _torch()
         B, D1, V = target.shape
         D = D1 - 1
@@ -403,7 +407,21 @@ class HipSampler:
         o = _abi.MtpOutputs()
         o.out_ids, o.out_count, o.accept_count, o.flags = (out_ids.data_ptr(), out_n.data_ptr(),
                                                           acc.data_ptr(), fl.data_ptr())
-        _abi.check(self.L.axs_mtp_verify(self.ctx, C.byref(d), C.byref(o), self._stream(stream)))
+        if options is None:
+            _abi.check(self.L.axs_mtp_verify(self.ctx, C.byref(d), C.byref(o), self._stream(stream)))
+            return MtpResult(out_ids, out_n, acc, fl, tuple(keep))
+        op = _abi.MtpOptions()
+        for name, dt in (("sources", np.uint32), ("pending_log_probs", np.float32), ("predicted", np.uint32)):
+            v = options.get(name)
+            if v is not None:
+                t = v if isinstance(v, torch.Tensor) else _dev_bytes(np.asarray(v, dtype=dt), self.device)
+                keep.append(t)
+                setattr(op, name, t.data_ptr())
+        op.model_mode = int(options.get("model_mode", _abi.MTP_MODEL_REJECTION))
+        op.ngram_mode = int(options.get("ngram_mode", _abi.MTP_NGRAM_CONFIDENCE))
+        op.lnq_mode = int(options.get("lnq_mode", _abi.MTP_LNQ_DISTRIBUTION))
+        op.delta_correction = int(bool(options.get("delta_correction", False)))
+        _abi.check(self.L.axs_mtp_verify_ex(self.ctx, C.byref(d), C.byref(op), C.byref(o), self._stream(stream)))
         return MtpResult(out_ids, out_n, acc, fl, tuple(keep))
 
 

@@ -176,6 +176,14 @@ struct KArgs {
     // and temperature of each row; the row's law is the untruncated softmax
     const uint32_t* lp_tokens;
     const float* lp_temps;
+    // MTP verify options (axs_mtp_verify_ex); mtp_stream: uniforms in the
+    // reference's stream order (else the slot layout of axs_mtp_verify)
+    const uint32_t* mtp_sources;  // [batch, depth] or NULL
+    const float* mtp_lnq_in;      // [batch, depth] or NULL
+    const uint32_t* mtp_pred;     // [batch, depth] or NULL
+    const float* mtp_lnq_full;    // [batch, depth] full-softmax ln q, or NULL
+    uint32_t* mtp_amax;           // [rows] each pipeline row's first argmax, or NULL
+    int32_t mtp_model_mode, mtp_ngram_mode, mtp_delta, mtp_stream;
     int64_t stride;
     const axs_sampling_params* params;
     const axs_sampling_params* params2;
@@ -256,11 +264,51 @@ __device__ __forceinline__ axs_sampling_params row_params(const KArgs& a, int r)
     return a.params[r];
 }
 
+// The draft source of position i of sequence b (AXS_MTP_SRC_DEFAULT and
+// unknown codes read as a model draft) and whether it carries a draft
+// distribution (MtpDraftSource::is_model_draft,
+// crates/ax-engine-mlx/src/runner/mtp_routing.rs:24-30).
+__device__ __forceinline__ uint32_t mtp_source(const KArgs& a, int b, int i) {
+    const uint32_t s = a.mtp_sources ? a.mtp_sources[(size_t)b * a.mtp_depth + i] : AXS_MTP_SRC_MTP;
+    return (s == AXS_MTP_SRC_GEMMA || s == AXS_MTP_SRC_NGRAM || s == AXS_MTP_SRC_HYBRID) ? s : AXS_MTP_SRC_MTP;
+}
+// Whether position i of sequence b is decided by a rejection test (and so
+// consumes a uniform) rather than a greedy comparison: not a greedy-mode
+// position, a finite draft log-prob, and target probabilities (target
+// temperature > 0) (runner/mod.rs:12355-12392).  Known before any
+// outcome: a model draft's ln q is always finite (floored at -30).
+__device__ __forceinline__ bool mtp_is_test(const KArgs& a, int b, int i, float target_temp) {
+    const uint32_t src = mtp_source(a, b, i);
+    const bool has_dd = src != AXS_MTP_SRC_NGRAM;
+    if (src == AXS_MTP_SRC_NGRAM && a.mtp_ngram_mode == AXS_MTP_NGRAM_GREEDY) return false;
+    if (has_dd && a.mtp_model_mode == AXS_MTP_MODEL_GREEDY) return false;
+    if (!(target_temp > 0.0f)) return false;
+    if (a.mtp_lnq_in) return isfinite(a.mtp_lnq_in[(size_t)b * a.mtp_depth + i]);
+    return has_dd || a.mtp_ngram_mode == AXS_MTP_NGRAM_DELTA;
+}
+// The k-th uniform of MTP sequence b: supplied [batch, depth + 1], or
+// Philox counter (b, step, 1 + k/4), word k % 4.
+__device__ __forceinline__ float mtp_uniform(const KArgs& a, int b, const axs_sampling_params& tp, uint32_t k) {
+    const int D = a.mtp_depth;
+    if (a.uniforms) return a.uniforms[(size_t)b * (D + 1) + k];
+    return philox_uniform(tp.seed, (uint32_t)b, tp.step, 1u + k / 4u, k & 3u);
+}
+
 // the uniform a row's draw consumes: supplied, or Philox(seed, row, step)
 __device__ __forceinline__ float row_uniform(const KArgs& a, int r, const axs_sampling_params& p) {
     if (a.mtp_depth > 0) {
         int D = a.mtp_depth;
         int nt = a.mtp_batch * (D + 1);
+        if (a.mtp_stream) {
+            // every target row j draws: it is the tail when the verify stops
+            // at position j (or j = D, the bonus), after the rejection tests
+            // of positions 0..min(j, D-1), which consume the first uniforms
+            if (r >= nt) return 0.5f;
+            const int b = r / (D + 1), j = r % (D + 1);
+            uint32_t k = 0;
+            for (int i = 0; i <= j && i < D; ++i) k += mtp_is_test(a, b, i, p.temperature) ? 1u : 0u;
+            return mtp_uniform(a, b, p, k);
+        }
         if (r >= nt || (r % (D + 1)) != D) return 0.5f;  // only the bonus row draws
         int b = r / (D + 1);
         if (a.uniforms) return a.uniforms[(size_t)b * (D + 1) + D];
@@ -1234,6 +1282,7 @@ __device__ __forceinline__ void finish_row(const KArgs& a, int r, int nseg, FinL
         gs = block_sum_d<NT>(gs, F.rd);
     }
     const Cand* pool = a.pool + (size_t)r * nseg * CAPS;
+    if (a.mtp_amax && tid == 0) a.mtp_amax[r] = am == NONE ? 0u : am;  // argmax_f32 (all-NaN: 0)
     finish_decide<NT>(a, r, row_params(a, r), m, am, fl, gs, ntot, F, [&](auto&& f) {
         for (uint32_t i = tid; i < (uint32_t)nseg * CAPS; i += NT) {
             if (i % CAPS >= F.cnt[i / CAPS]) continue;
@@ -2526,6 +2575,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     uint32_t am = lane < RWV ? SL.wa[lane] : NONE;
     wave_argmax_dpp(m, am);
     if (am == NONE) m = -INFINITY;
+    if (a.mtp_amax && tid == 0) a.mtp_amax[r] = am == NONE ? 0u : am;  // argmax_f32 (all-NaN: 0)
     double gsum = 0.0;
     if (gsum_on && isfinite(m)) {
 #pragma unroll
@@ -3252,6 +3302,20 @@ __global__ __launch_bounds__(NT_EX) void k_exact_row(KArgs a) {
 // (crates/ax-engine-mlx/src/runner/mod.rs:12388-12431, sampling.rs:709-752)
 // --------------------------------------------------------------------------
 constexpr int NT_MTP = 1024;
+// One 1024-thread workgroup per sequence.  Per draft position i, in order:
+// a greedy comparison of the draft with the target's prediction (the mode
+// gates, or no target probabilities / no finite draft log-prob), or the
+// rejection test u < min(1, P_i(d) / q') with q' = max(exp(ln q * Td/Tt),
+// 1e-37) (the temperature ratio for model drafts only, when the two differ)
+// (runner/mod.rs:12355-12446).  A rejected test is corrected by the residual
+// max(P_i - Q_i, 0) over the id-ascending union (Q_i = delta(draft) for an
+// n-gram draft when delta_correction is set) or, for an n-gram draft
+// without it, left to the target row's own draw; a failed comparison is
+// corrected by the prediction.  The tail (runner/mod.rs:9732-9775): the
+// correction, else the bonus draw of target row D, else the draw of the
+// target row at the rejected position.  With a.mtp_stream the uniforms are
+// taken in the reference's stream order; otherwise slot i for position i's
+// test and slot D for the tail (axs_mtp_verify).
 __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* draft_ids,
                                                        uint32_t* out_ids, uint32_t* out_count,
                                                        uint32_t* out_accept, uint32_t* out_flags) {
@@ -3262,6 +3326,7 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
     __shared__ int s_ft, s_fd;
     __shared__ float s_rsum;
     __shared__ uint32_t s_rn;
+    __shared__ uint32_t s_corr;
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
     const int D = a.mtp_depth;
@@ -3270,21 +3335,42 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
     const axs_sampling_params tp = a.params[b];
     const axs_sampling_params dp = a.params2[b];
     const float Tt = tp.temperature, Td = dp.temperature;
+    const bool stream = a.mtp_stream != 0;
+    constexpr uint32_t NEAR_DIST = AXS_FLAG_NEAR_NUCLEUS | AXS_FLAG_NEAR_MINP | AXS_FLAG_NEAR_TIE;
+    constexpr uint32_t NEAR_ALL = NEAR_DIST | AXS_FLAG_NEAR_DRAW;
     uint32_t flags = 0;
-    uint32_t count = 0;
+    uint32_t count = 0;    // accepted drafts
+    uint32_t nu = 0;       // uniforms consumed (stream order)
+    uint32_t corr = NONE;  // the correction token
+    int tail_row = -1;     // position whose target row's own draw is the tail
+    bool stopped = false;
     for (int i = 0; i < D; ++i) {
         const int tr = b * (D + 1) + i;
         const int dr = Bm * (D + 1) + b * D + i;
-        const RowState rt = a.rstate[tr];
-        const RowState rd = a.rstate[dr];
-        if ((rt.flags | rd.flags) & AXS_FLAG_ERROR || rt.nlist < rt.kept || rd.nlist < rd.kept) {
-            flags |= AXS_MTP_FLAG_ERROR;
+        const uint32_t src = stream ? mtp_source(a, b, i) : (uint32_t)AXS_MTP_SRC_MTP;
+        const bool has_dd = src != AXS_MTP_SRC_NGRAM;
+        const uint32_t d = draft_ids[(size_t)b * D + i];
+        if (stream && !mtp_is_test(a, b, i, Tt)) {
+            // greedy comparison with the target's prediction
+            const uint32_t pred = a.mtp_pred ? a.mtp_pred[(size_t)b * D + i] : a.mtp_amax[tr];
+            if (pred == d) {
+                if (tid == 0) out_ids[(size_t)b * (D + 1) + count] = d;
+                ++count;
+                continue;
+            }
+            corr = pred;
+            flags |= AXS_MTP_FLAG_CORRECTION;
+            stopped = true;
             break;
         }
-        if ((rt.flags | rd.flags) & (AXS_FLAG_NEAR_DRAW | AXS_FLAG_NEAR_NUCLEUS | AXS_FLAG_NEAR_MINP |
-                                     AXS_FLAG_NEAR_TIE))
-            flags |= AXS_MTP_FLAG_NEAR;
-        const uint32_t d = draft_ids[(size_t)b * D + i];
+        const RowState rt = a.rstate[tr];
+        const RowState rd = has_dd ? a.rstate[dr] : rt;
+        if ((rt.flags | rd.flags) & AXS_FLAG_ERROR || rt.nlist < rt.kept || rd.nlist < rd.kept) {
+            flags |= AXS_MTP_FLAG_ERROR;
+            stopped = true;
+            break;
+        }
+        if ((rt.flags | rd.flags) & NEAR_DIST) flags |= AXS_MTP_FLAG_NEAR;
         const uint32_t* tid_l = a.ws_kept_id + (size_t)tr * KEPT_CAP;
         const float* tp_l = a.ws_kept_p + (size_t)tr * KEPT_CAP;
         const uint32_t* did_l = a.ws_kept_id + (size_t)dr * KEPT_CAP;
@@ -3299,22 +3385,28 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         __syncthreads();
         for (uint32_t k = tid; k < rt.nlist; k += NT_MTP)
             if (tid_l[k] == d) atomicMax(&s_ft, (int)k);
-        for (uint32_t k = tid; k < rd.nlist; k += NT_MTP)
-            if (did_l[k] == d) atomicMax(&s_fd, (int)k);
+        if (has_dd)
+            for (uint32_t k = tid; k < rd.nlist; k += NT_MTP)
+                if (did_l[k] == d) atomicMax(&s_fd, (int)k);
         __syncthreads();
         // normalised entries p / F (TokenDistribution::new, sampling.rs:128-144)
-        float qd = s_fd >= 0 ? __fdiv_rn(dp_l[s_fd], rd.F) : 0.0f;
-        float pt = s_ft >= 0 ? __fdiv_rn(tp_l[s_ft], rt.F) : 0.0f;
-        pt = fmaxf(pt, 0.0f);
-        float lnq = logprob_of(qd);
+        const float pt = fmaxf(s_ft >= 0 ? __fdiv_rn(tp_l[s_ft], rt.F) : 0.0f, 0.0f);
+        float lnq;
+        if (a.mtp_lnq_in) {
+            lnq = a.mtp_lnq_in[(size_t)b * D + i];
+        } else if (!has_dd) {
+            lnq = 0.0f;  // an n-gram draft under the delta law
+        } else if (a.mtp_lnq_full) {
+            lnq = a.mtp_lnq_full[(size_t)b * D + i];
+        } else {
+            lnq = logprob_of(s_fd >= 0 ? __fdiv_rn(dp_l[s_fd], rd.F) : 0.0f);
+        }
         float lps = lnq;
-        if (Td > 0.0f && Tt > 0.0f && fabsf(__fsub_rn(Td, Tt)) > 1e-6f)
+        if (has_dd && Td > 0.0f && Tt > 0.0f && fabsf(__fsub_rn(Td, Tt)) > 1e-6f)
             lps = __fmul_rn(lnq, __fdiv_rn(Td, Tt));
-        float pdraft = fmaxf(exp_ref(lps), 1e-37f);
-        float accp = fminf(__fdiv_rn(pt, pdraft), 1.0f);
-        float u = a.uniforms ? a.uniforms[(size_t)b * (D + 1) + i]
-                             : philox_uniform(tp.seed, (uint32_t)b, tp.step, 1u + (uint32_t)i / 4u,
-                                              (uint32_t)i & 3u);
+        const float pdraft = fmaxf(exp_ref(lps), 1e-37f);
+        const float accp = fminf(__fdiv_rn(pt, pdraft), 1.0f);
+        const float u = mtp_uniform(a, b, tp, stream ? nu++ : (uint32_t)i);
         // u >= 1 never accepts, whatever accp <= 1 rounds to
         if (u < 1.0f && fabs((double)u - (double)accp) < 1e-6) flags |= AXS_MTP_FLAG_NEAR_ACCEPT;
         if (u < accp) {
@@ -3322,21 +3414,29 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
             ++count;
             continue;
         }
+        stopped = true;
+        if (!has_dd && !a.mtp_delta) {
+            tail_row = i;  // no correction: the target row's own draw (sample_logit_row)
+            break;
+        }
         // residual max(P - Q, 0) over the union of ids, ascending id order
-        // (runner/mod.rs:12409-12431, sampling.rs:709-752).  An id only in
-        // the draft carries max(0 - q, 0) = 0 and is skipped, so the walk is
-        // over the target's ids: both lists sorted by id, each target term
-        // with its draft entry found by binary search, all in parallel; the
+        // (runner/mod.rs:12409-12431, sampling.rs:709-752; Q = delta(draft)
+        // for an n-gram draft: runner/mod.rs:12161-12184).  An id only in Q
+        // carries max(0 - q, 0) = 0 and is skipped, so the walk is over the
+        // target's ids: both lists sorted by id, each target term with its
+        // draft entry found by binary search, all in parallel; the
         // reference's sequential f32 sums run on one thread over LDS.
-        const float ut = a.uniforms ? a.uniforms[(size_t)b * (D + 1) + D]
-                                    : philox_uniform(tp.seed, (uint32_t)b, tp.step,
-                                                     1u + (uint32_t)D / 4u, (uint32_t)D & 3u);
-        const uint32_t nt = rt.nlist, nd = rd.nlist;
+        const float ut = mtp_uniform(a, b, tp, stream ? nu : (uint32_t)D);
+        const uint32_t nt = rt.nlist, nd = has_dd ? rd.nlist : 1u;
         uint32_t npt = next_pow2(nt > 0 ? nt : 1), npd = next_pow2(nd > 0 ? nd : 1);
         for (uint32_t k = tid; k < npt; k += NT_MTP)
             s_t[k] = k < nt ? (((uint64_t)(~tid_l[k]) << 32) | __float_as_uint(__fdiv_rn(tp_l[k], rt.F))) : 0ull;
-        for (uint32_t k = tid; k < npd; k += NT_MTP)
-            s_d[k] = k < nd ? (((uint64_t)(~did_l[k]) << 32) | __float_as_uint(__fdiv_rn(dp_l[k], rd.F))) : 0ull;
+        if (has_dd) {
+            for (uint32_t k = tid; k < npd; k += NT_MTP)
+                s_d[k] = k < nd ? (((uint64_t)(~did_l[k]) << 32) | __float_as_uint(__fdiv_rn(dp_l[k], rd.F))) : 0ull;
+        } else if (tid == 0) {
+            s_d[0] = ((uint64_t)(~d) << 32) | __float_as_uint(1.0f);
+        }
         __syncthreads();
         block_sort_desc<NT_MTP>(s_t, npt);  // descending ~id = ascending id
         block_sort_desc<NT_MTP>(s_d, npd);
@@ -3368,7 +3468,6 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         }
         __syncthreads();
         const float rsum = s_rsum;
-        uint32_t nw = nt;  // terms of the walk (s_v: value, or -1 for a skipped id)
         if (s_rn > 0 && rsum > 0.0f && isfinite(rsum)) {
             // normalised residual, then sample_from_token_distribution
             for (uint32_t k = tid; k < nt; k += NT_MTP) {
@@ -3385,14 +3484,14 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         __syncthreads();
         if (tid == 0) {
             float total = 0.0f;
-            for (uint32_t k = 0; k < nw; ++k) {
+            for (uint32_t k = 0; k < nt; ++k) {
                 const float q = s_v[k];
                 if (!(q < 0.0f)) total = __fadd_rn(total, q);
             }
             const float thr = __fmul_rn(ut, total);
             float cum = 0.0f, bp = -1.0f;
-            uint32_t last_id = NONE, corr = NONE;
-            for (uint32_t k = 0; k < nw; ++k) {
+            uint32_t last_id = NONE, cr = NONE;
+            for (uint32_t k = 0; k < nt; ++k) {
                 const float q = s_v[k];
                 if (q < 0.0f) continue;
                 cum = __fadd_rn(cum, q);
@@ -3401,39 +3500,41 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
                     last_id = s_id[k];
                 }
                 if (cum >= thr) {
-                    corr = s_id[k];
+                    cr = s_id[k];
                     break;
                 }
             }
-            if (corr == NONE) corr = last_id;
-            out_ids[(size_t)b * (D + 1) + count] = corr;
+            s_corr = cr == NONE ? last_id : cr;
         }
-        ++count;
+        __syncthreads();
+        corr = s_corr;
         flags |= AXS_MTP_FLAG_RESIDUAL;
         break;
     }
-    if (tid == 0) {
-        uint32_t acc = 0;
-        if (!(flags & (AXS_MTP_FLAG_RESIDUAL | AXS_MTP_FLAG_ERROR))) {
-            // all drafts accepted: the bonus token of target row D
-            const int br = b * (D + 1) + D;
-            const RowState rb = a.rstate[br];
+    if (tid != 0) return;
+    uint32_t acc = count;
+    if (!(flags & AXS_MTP_FLAG_ERROR)) {
+        uint32_t tail = corr;
+        if (!stopped || tail_row >= 0) {
+            // all drafts accepted: the bonus draw of target row D; or the
+            // target row at the rejected position
+            const int j = stopped ? tail_row : D;
+            const RowState rb = a.rstate[b * (D + 1) + j];
             if (rb.flags & AXS_FLAG_ERROR) flags |= AXS_MTP_FLAG_ERROR;
-            if (rb.flags & (AXS_FLAG_NEAR_DRAW | AXS_FLAG_NEAR_NUCLEUS | AXS_FLAG_NEAR_MINP |
-                            AXS_FLAG_NEAR_TIE))
-                flags |= AXS_MTP_FLAG_NEAR;
-            out_ids[(size_t)b * (D + 1) + count] = a.out_ids[br];
-            acc = count;
-            ++count;
-            flags |= AXS_MTP_FLAG_BONUS;
-        } else {
-            acc = count > 0 ? count - 1 : 0;
+            if (rb.flags & NEAR_ALL) flags |= AXS_MTP_FLAG_NEAR;
+            tail = a.out_ids[b * (D + 1) + j];
+            flags |= stopped ? AXS_MTP_FLAG_TAIL_ROW : AXS_MTP_FLAG_BONUS;
         }
-        if (flags & AXS_MTP_FLAG_ERROR) count = 0;
-        out_count[b] = count;
-        if (out_accept) out_accept[b] = acc;
-        if (out_flags) out_flags[b] = flags;
+        out_ids[(size_t)b * (D + 1) + count] = tail;
+        ++count;
     }
+    if (flags & AXS_MTP_FLAG_ERROR) {
+        count = 0;
+        acc = 0;
+    }
+    out_count[b] = count;
+    if (out_accept) out_accept[b] = acc;
+    if (out_flags) out_flags[b] = flags;
 }
 
 }  // namespace axs
@@ -3496,6 +3597,10 @@ struct axs_context {
     uint32_t* kept_id;
     float* kept_p;
     uint32_t* mtp_tok;  // per-row tokens of the MTP sampler pass
+    uint32_t* mtp_amax; // per-row first argmax of the MTP sampler pass
+    float* mtp_lnq;     // full-softmax draft log-probs [rows]
+    uint32_t* lp_tok;   // token echo of the draft log-prob pass [rows]
+    float* lp_temps;    // draft temperatures per draft row [rows]
     bool timing;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev[AXS_KERNEL_COUNT];
     // Calls are serialised: the lock covers each call's enqueue, and a call
@@ -3548,7 +3653,7 @@ void free_ctx(axs_context* c) {
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     void* ptrs[] = {c->cstat, c->pool, c->rstate,  c->exact_rows, c->exact_count,
                     c->row_done, c->dense, c->ckey, c->ckey2, c->tmp64, c->sbuf, c->bend,
-                    c->kept_id, c->kept_p, c->mtp_tok};
+                    c->kept_id, c->kept_p, c->mtp_tok, c->mtp_amax, c->mtp_lnq, c->lp_tok, c->lp_temps};
     for (void* q : ptrs)
         if (q) (void)hipFree(q);
     delete c;
@@ -3910,7 +4015,8 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
         (rc = dalloc(&c->ckey2, R * Vv)) || (rc = dalloc(&c->tmp64, R * (size_t)c->tmp_stride)) ||
         (rc = dalloc(&c->sbuf, R * Vv)) || (rc = dalloc(&c->bend, R * NBUCKET)) ||
         (rc = dalloc(&c->kept_id, R * KEPT_CAP)) || (rc = dalloc(&c->kept_p, R * KEPT_CAP)) ||
-        (rc = dalloc(&c->mtp_tok, R))) {
+        (rc = dalloc(&c->mtp_tok, R)) || (rc = dalloc(&c->mtp_amax, R)) || (rc = dalloc(&c->mtp_lnq, R)) ||
+        (rc = dalloc(&c->lp_tok, R)) || (rc = dalloc(&c->lp_temps, R))) {
         free_ctx(c);
         return rc;
     }
@@ -4211,7 +4317,19 @@ int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int
     return order_end(ctx, s);
 }
 
-int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_outputs* o, void* stream) {
+}  // extern "C"
+
+namespace {
+
+// target temperatures of the draft rows (row b * depth + i: sequence b's
+// draft temperature) for the full-softmax draft log-prob pass
+__global__ void k_draft_temps(const axs_sampling_params* dp, int depth, int n, float* out) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = dp[i / depth].temperature;
+}
+
+int mtp_verify_impl(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_options* op,
+                    const axs_mtp_outputs* o, void* stream) {
     if (!ctx || !d || !o) return fail(AXS_E_INVALID, "ctx, desc and outputs must be non-NULL");
     if (!d->target_logits || !d->draft_logits || !d->draft_ids || !d->target_params ||
         !d->draft_params || !o->out_ids || !o->out_count)
@@ -4219,14 +4337,40 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_output
     if (d->dtype != AXS_DTYPE_F32 && d->dtype != AXS_DTYPE_BF16) return fail(AXS_E_INVALID, "bad dtype");
     if (d->batch < 1 || d->vocab < 1 || d->depth < 1 || d->depth > 7 || d->row_stride < d->vocab)
         return fail(AXS_E_INVALID, "bad shape (depth must be 1..7)");
-    int64_t rows = (int64_t)d->batch * (2 * d->depth + 1);
+    if (op && (op->model_mode < AXS_MTP_MODEL_GREEDY || op->model_mode > AXS_MTP_MODEL_REJECTION ||
+               op->ngram_mode < AXS_MTP_NGRAM_CONFIDENCE || op->ngram_mode > AXS_MTP_NGRAM_GREEDY ||
+               op->lnq_mode < AXS_MTP_LNQ_DISTRIBUTION || op->lnq_mode > AXS_MTP_LNQ_FULL_SOFTMAX))
+        return fail(AXS_E_INVALID, "bad MTP option mode");
+    const int64_t rows = (int64_t)d->batch * (2 * d->depth + 1);
     if (rows > ctx->max_rows || d->vocab > ctx->max_vocab)
         return fail(AXS_E_CAPACITY, "batch*(2*depth+1) rows or vocab larger than the context");
     std::lock_guard<std::mutex> lk(ctx->mu);
     DevGuard g(ctx->device);
     hipStream_t s = (hipStream_t)stream;
-    int rc0 = order_begin(ctx, s);
-    if (rc0) return rc0;
+    int rc = order_begin(ctx, s);
+    if (rc) return rc;
+    const bool ex = op != nullptr;
+    const bool full_lnq = ex && op->lnq_mode == AXS_MTP_LNQ_FULL_SOFTMAX && !op->pending_log_probs;
+    if (full_lnq) {
+        // ln softmax(draft row / T_d)[d] of every draft row, the draft's own
+        // temperature per sequence (axs_token_logprob_batch's pass)
+        const int nd = d->batch * d->depth;
+        hipLaunchKernelGGL(k_draft_temps, dim3((unsigned)((nd + 255) / 256)), dim3(256), 0, s, d->draft_params,
+                           d->depth, nd, ctx->lp_temps);
+        KArgs l{};
+        l.logits = d->draft_logits;
+        l.dtype = d->dtype;
+        l.nrows = nd;
+        l.vocab = d->vocab;
+        l.stride = d->row_stride;
+        l.params = nullptr;
+        l.lp_tokens = d->draft_ids;
+        l.lp_temps = ctx->lp_temps;
+        l.out_ids = ctx->lp_tok;
+        l.out_lp = ctx->mtp_lnq;
+        Plan lp = make_plan(d->dtype, nd, d->vocab, d->draft_logits, d->row_stride, nullptr);
+        if ((rc = run_pipeline(ctx, l, lp, s))) return rc;
+    }
     KArgs a{};
     a.logits = d->target_logits;
     a.logits2 = d->draft_logits;
@@ -4243,15 +4387,42 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_output
     a.ws_kept_id = ctx->kept_id;
     a.ws_kept_p = ctx->kept_p;
     a.out_ids = ctx->mtp_tok;
+    a.mtp_amax = ctx->mtp_amax;
+    if (ex) {
+        a.mtp_stream = 1;
+        a.mtp_sources = op->sources;
+        a.mtp_lnq_in = op->pending_log_probs;
+        a.mtp_pred = op->predicted;
+        a.mtp_lnq_full = full_lnq ? ctx->mtp_lnq : nullptr;
+        a.mtp_model_mode = op->model_mode;
+        a.mtp_ngram_mode = op->ngram_mode;
+        a.mtp_delta = op->delta_correction ? 1 : 0;
+    } else {
+        a.mtp_model_mode = AXS_MTP_MODEL_REJECTION;
+    }
     Plan pl = make_plan(d->dtype, (int)rows, d->vocab, d->target_logits, d->row_stride, d->draft_logits);
-    int rc = run_pipeline(ctx, a, pl, s);
-    if (rc) return rc;
+    if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
     timed(ctx, AXS_KERNEL_MTP, s, [&] {
         hipLaunchKernelGGL(k_mtp_verify, dim3((unsigned)d->batch), dim3(NT_MTP), 0, s, a, d->draft_ids,
                            o->out_ids, o->out_count, o->accept_count, o->flags);
     });
     AXS_HIP_CHECK(hipGetLastError());
     return order_end(ctx, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_outputs* o, void* stream) {
+    return mtp_verify_impl(ctx, d, nullptr, o, stream);
+}
+
+int axs_mtp_verify_ex(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_options* opts,
+                      const axs_mtp_outputs* o, void* stream) {
+    axs_mtp_options dflt{};
+    dflt.model_mode = AXS_MTP_MODEL_REJECTION;
+    return mtp_verify_impl(ctx, d, opts ? opts : &dflt, o, stream);
 }
 
 int axs_timing_enable(axs_context* ctx, int enable) {

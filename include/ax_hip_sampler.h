@@ -210,6 +210,11 @@ typedef struct axs_mtp_desc {
 #define AXS_MTP_FLAG_BONUS       (1u << 1)  /* all drafts accepted, bonus drawn  */
 #define AXS_MTP_FLAG_NEAR_ACCEPT (1u << 2)  /* |u - p/q| < 1e-6 at a decision   */
 #define AXS_MTP_FLAG_NEAR        (1u << 3)  /* a distribution had a near flag   */
+#define AXS_MTP_FLAG_CORRECTION  (1u << 4)  /* tail = the target's prediction
+                                               after a greedy comparison failed */
+#define AXS_MTP_FLAG_TAIL_ROW    (1u << 5)  /* tail = the draw of the target row
+                                               at the rejected position (no
+                                               correction: an n-gram draft)   */
 #define AXS_MTP_FLAG_ERROR       (1u << 31)
 
 typedef struct axs_mtp_outputs {
@@ -218,6 +223,53 @@ typedef struct axs_mtp_outputs {
     uint32_t* accept_count;  /* [batch] or NULL                                  */
     uint32_t* flags;         /* [batch] or NULL                                  */
 } axs_mtp_outputs;
+
+/*
+ * Options of axs_mtp_verify_ex: the rest of mtp_accept_count's contract
+ * (crates/ax-engine-mlx/src/runner/mod.rs:12333-12462) — per-position draft
+ * sources, the model and n-gram acceptance modes, caller-supplied draft
+ * log-probs and target predictions — and the full-softmax draft log-prob.
+ */
+#define AXS_MTP_SRC_DEFAULT 0  /* as AXS_MTP_SRC_MTP (the reference's None)   */
+#define AXS_MTP_SRC_MTP     1  /* MtpDraftSource (crates/ax-engine-mlx/src/   */
+#define AXS_MTP_SRC_GEMMA   2  /* runner/mtp_routing.rs:15-33): MTP head,     */
+#define AXS_MTP_SRC_NGRAM   3  /* Gemma4 assistant, n-gram, hybrid MTP tail;  */
+#define AXS_MTP_SRC_HYBRID  4  /* all but n-gram carry a draft distribution   */
+#define AXS_MTP_MODEL_GREEDY     0  /* MtpModelAcceptanceMode (:79-83)         */
+#define AXS_MTP_MODEL_REJECTION  1
+#define AXS_MTP_NGRAM_CONFIDENCE 0  /* MtpNgramAcceptanceMode (:61-66)         */
+#define AXS_MTP_NGRAM_DELTA      1
+#define AXS_MTP_NGRAM_GREEDY     2
+#define AXS_MTP_LNQ_DISTRIBUTION 0  /* ln q = ln Q_i(d), Q_i = token_distribution
+                                       of draft row i (the filtered law)      */
+#define AXS_MTP_LNQ_FULL_SOFTMAX 1  /* ln q = ln softmax(draft row i / T_d)[d],
+                                       the full-vocabulary law of
+                                       gpu_draft_log_prob_lazy
+                                       (crates/ax-engine-mlx/src/mtp.rs:203-220),
+                                       as axs_token_logprob_batch computes it */
+typedef struct axs_mtp_options {
+    const uint32_t* sources;            /* [batch, depth] AXS_MTP_SRC_*, or NULL:
+                                           every position a model draft          */
+    const float*    pending_log_probs;  /* [batch, depth] ln q per position, or
+                                           NULL: computed for model drafts
+                                           (lnq_mode); for n-gram drafts 0.0
+                                           under AXS_MTP_NGRAM_DELTA, else NaN
+                                           (no log-prob: greedy comparison)      */
+    const uint32_t* predicted;          /* [batch, depth] the target's token per
+                                           position for the greedy comparisons,
+                                           or NULL: target row i's first argmax  */
+    int32_t model_mode;                 /* AXS_MTP_MODEL_*                        */
+    int32_t ngram_mode;                 /* AXS_MTP_NGRAM_*                        */
+    int32_t lnq_mode;                   /* AXS_MTP_LNQ_*                          */
+    int32_t delta_correction;           /* nonzero: a rejected draft without a
+                                           draft distribution (n-gram) is
+                                           corrected by the residual of the
+                                           target against delta(draft)
+                                           (sample_exact_mtp_delta_rejection_
+                                           correction, runner/mod.rs:12161-12184);
+                                           zero: no correction, the tail is the
+                                           target row's own draw                 */
+} axs_mtp_options;
 
 typedef struct axs_context axs_context;
 
@@ -302,6 +354,23 @@ int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int
                             float* out_logprob, void* stream);
 
 /* MTP speculative verify (see axs_mtp_desc). */
+/* MTP verify with options: per sequence, mtp_accept_count
+ * (crates/ax-engine-mlx/src/runner/mod.rs:12333-12462) over the draft ids,
+ * with target probabilities P_i(d) = token_distribution(target row i)(d)
+ * when the target temperature is > 0 (none otherwise: greedy comparisons),
+ * target distributions P_i and draft distributions Q_i (model drafts), then
+ * the tail (runner/mod.rs:9732-9775, ngram_accel.rs:1543-1590): the
+ * correction when there is one, the draw of target row depth when every
+ * draft was accepted (bonus), else the draw of the target row at the
+ * rejected position.  Uniforms follow the reference's stream: uniforms[b, k]
+ * is the k-th uniform sequence b consumes (each rejection test, then the
+ * residual or the tail draw), NULL = Philox (b, step, 1 + k/4, word k%4).
+ * opts NULL: every position a model draft under rejection sampling, ln q
+ * from the draft distributions (axs_mtp_verify's law, with the stream order
+ * of uniforms). */
+int axs_mtp_verify_ex(axs_context* ctx, const axs_mtp_desc* desc, const axs_mtp_options* opts,
+                      const axs_mtp_outputs* out, void* stream);
+
 int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
                    const axs_mtp_outputs* out, void* stream);
 

@@ -55,6 +55,7 @@ def test_struct_layouts_match_the_header():
     assert ctypes.sizeof(_abi.Outputs) == 48
     assert ctypes.sizeof(_abi.MtpDesc) == 72
     assert ctypes.sizeof(_abi.MtpOutputs) == 32
+    assert ctypes.sizeof(_abi.MtpOptions) == 40
 
 
 def test_c_struct_sizes_from_the_compiler(tmp_path):
@@ -63,11 +64,11 @@ def test_c_struct_sizes_from_the_compiler(tmp_path):
         '#include "ax_hip_sampler.h"\n#include <stdio.h>\n#include <stddef.h>\n'
         "int main(){printf(\"%zu %zu %zu %zu %zu\\n\", sizeof(axs_sampling_params),"
         " sizeof(axs_batch_desc), sizeof(axs_outputs), sizeof(axs_mtp_desc),"
-        " sizeof(axs_mtp_outputs));return 0;}\n")
+        " sizeof(axs_mtp_outputs)); printf(\"%zu\\n\", sizeof(axs_mtp_options)); return 0;}\n")
     exe = tmp_path / "s"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     sizes = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
-    assert sizes == ["64", "120", "48", "72", "32"]
+    assert sizes == ["64", "120", "48", "72", "32", "40"]
 
 
 def test_error_handler_and_last_error_without_a_gpu():

@@ -12,6 +12,8 @@ either side, so the empty-residual fallback of draft == target is held
 exactly.  Draft ids are drawn
 from the draft law by the oracle with its own uniforms (config C5).
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -199,3 +201,147 @@ def test_index_order_laws_with_zero_probabilities(sampler, oracle):
     dids = _draft_ids(oracle, d, DTYPE_F32, B, D, V, dp, 61)
     us = rng.random((B, D + 1)).astype(np.float32)
     _run(sampler, oracle, t, d, DTYPE_F32, tp, dp, dids, us, "index-order with p = 0")
+
+
+# --- axs_mtp_verify_ex: mtp_accept_count's modes, sources and tail ----------------
+
+
+def _mtp_expect(oracle, tf, df, dids, tp, dp, us, opts, D):
+    """The reference law for one sequence with the oracle's pieces:
+    axo_mtp_accept_count (crates/ax-engine-mlx/src/runner/mod.rs:12333-12462)
+    over P_i / Q_i = token_distribution, then the tail
+    (runner/mod.rs:9732-9775): correction, bonus draw of row D, or the draw
+    of the target row at the rejected position (delta residual for an n-gram
+    draft when delta_correction is set).  Returns (ids, accept_count)."""
+    from ax_sampler import _abi
+
+    Tt, Td = float(tp["temperature"][0]), float(dp["temperature"][0])
+    src = [int(x) if int(x) in (1, 2, 3, 4) else 1 for x in (opts.get("sources") if opts.get("sources") is not None
+                                                            else np.ones(D, np.uint32))]
+    P = [oracle.token_distribution(tf[i], tp) for i in range(D)]
+    Q = [oracle.token_distribution(df[i], dp) for i in range(D)]
+    lnq, tests = [], []
+    for i in range(D):
+        has_dd = src[i] != _abi.MTP_SRC_NGRAM
+        if opts.get("pending_log_probs") is not None:
+            v = float(opts["pending_log_probs"][i])
+        elif not has_dd:
+            v = 0.0 if opts.get("ngram_mode") == _abi.MTP_NGRAM_DELTA else float("nan")
+        elif opts.get("lnq_mode") == _abi.MTP_LNQ_FULL_SOFTMAX:
+            v = oracle.full_vocab_token_logprob(df[i], int(dids[i]), Td)
+        else:
+            v = oracle.logprob_of(oracle.distribution_prob(Q[i][0], Q[i][1], int(dids[i])))
+        lnq.append(v)
+        greedy = ((src[i] == _abi.MTP_SRC_NGRAM and opts.get("ngram_mode") == _abi.MTP_NGRAM_GREEDY) or
+                  (has_dd and opts.get("model_mode", 1) == _abi.MTP_MODEL_GREEDY))
+        tests.append((not greedy) and math.isfinite(v) and Tt > 0)
+    pred = (list(map(int, opts["predicted"])) if opts.get("predicted") is not None
+            else [oracle.argmax_f32(tf[i]) for i in range(D)])
+    tprobs = [max(oracle.distribution_prob(P[i][0], P[i][1], int(dids[i])), 0.0) for i in range(D)] if Tt > 0 else None
+    ac, allacc, corr = oracle.mtp_accept_count(
+        list(map(int, dids)), lnq, [Q[i] for i in range(D) if src[i] != _abi.MTP_SRC_NGRAM], src, tprobs, P,
+        pred, None, Td, Tt, opts.get("model_mode", 1), opts.get("ngram_mode", 0), uniforms=us)
+    k = sum(tests[: min(ac, D - 1) + 1]) if not allacc else sum(tests)
+    if allacc:
+        tail = oracle.sample_row(tf[D], tp, [], u=float(us[k]))[0]
+    elif corr is not None:
+        tail = corr
+    elif opts.get("delta_correction"):
+        tail = oracle.sample_residual(P[ac][0], P[ac][1], [int(dids[ac])], [1.0], float(us[k]))
+    else:
+        tail = oracle.sample_row(tf[ac], tp, [], u=float(us[k]))[0]
+    return list(map(int, dids[:ac])) + [int(tail)], ac
+
+
+def _ex_case(seed, B=16, D=3, V=4099):
+    rng = np.random.default_rng(seed)
+    t = rng.standard_normal((B, D + 1, V), dtype=np.float32) * np.float32(2.5)
+    d = t[:, :D, :] + rng.standard_normal((B, D, V), dtype=np.float32) * np.float32(0.6)
+    _, _, tp, dp = make_c5(48 + seed, B=B, depth=D, V=16)
+    tp["temperature"] = rng.choice(np.array([0.7, 1.0], np.float32), B)
+    dp["temperature"] = tp["temperature"] * rng.choice(np.array([1.0, 0.9], np.float32), B)
+    tp["top_k"], dp["top_k"] = 40, 40
+    tp["top_p"], dp["top_p"] = 0.95, 0.95
+    return rng, t, d, tp, dp
+
+
+@pytest.mark.parametrize("case", ["rejection", "modes", "full_lnq", "greedy_target", "supplied"])
+def test_mtp_verify_ex_matches_accept_count(sampler, oracle, case):
+    import torch
+
+    from ax_sampler import _abi
+
+    rng, t, d, tp, dp = _ex_case({"rejection": 1, "modes": 2, "full_lnq": 3, "greedy_target": 4, "supplied": 5}[case])
+    B, D1, V = t.shape
+    D = D1 - 1
+    dids = _draft_ids(oracle, d, DTYPE_F32, B, D, V, dp, 62)
+    opts = {"model_mode": _abi.MTP_MODEL_REJECTION}
+    if case == "modes" or case == "supplied":
+        opts["sources"] = rng.choice(np.array([0, 1, 2, 3, 4], np.uint32), (B, D))
+        opts["ngram_mode"] = int(rng.integers(0, 3))
+        opts["model_mode"] = int(rng.integers(0, 2))
+        opts["delta_correction"] = bool(rng.integers(0, 2))
+        # n-gram drafts: the target's argmax half of the time, else a random id
+        am = np.array([[oracle.argmax_f32(t[b, i]) for i in range(D)] for b in range(B)], np.uint32)
+        ng = opts["sources"] == 3
+        dids = np.where(ng & (rng.random((B, D)) < 0.5), am, np.where(ng, rng.integers(0, V, (B, D)), dids)
+                        ).astype(np.uint32)
+    if case == "supplied":
+        opts["pending_log_probs"] = np.where(rng.random((B, D)) < 0.2, np.nan,
+                                             -rng.random((B, D)) * 3).astype(np.float32)
+        opts["predicted"] = rng.integers(0, V, (B, D)).astype(np.uint32)
+    if case == "full_lnq":
+        opts["lnq_mode"] = _abi.MTP_LNQ_FULL_SOFTMAX
+    if case == "greedy_target":
+        tp["temperature"][: B // 2] = 0.0
+    us = rng.random((B, D + 1)).astype(np.float32)
+    res = sampler.mtp_verify(_to_dev(t, DTYPE_F32), _to_dev(d, DTYPE_F32), dids, tp, dp, uniforms=us,
+                             options=opts)
+    torch.cuda.synchronize()
+    g_ids, g_n, g_ac, g_fl = res.numpy()
+    near = 0
+    for b in range(B):
+        ob = {k: (v[b] if isinstance(v, np.ndarray) else v) for k, v in opts.items()}
+        want, ac = _mtp_expect(oracle, t[b], d[b], dids[b], tp[b:b + 1], dp[b:b + 1], us[b], ob, D)
+        got = g_ids[b, : g_n[b]].tolist()
+        assert not g_fl[b] & np.uint32(_abi.MTP_FLAG_ERROR), (case, b)
+        if g_fl[b] & np.uint32(_abi.MTP_FLAG_NEAR_ACCEPT):
+            near += 1
+            continue
+        assert got == want and g_ac[b] == ac, (case, b, got, want, int(g_ac[b]), ac, hex(int(g_fl[b])))
+    assert near <= boundary_allowance(B), near
+    log(f"mtp_verify_ex {case}: {B} sequences, near {near}, accepted {int(g_ac.sum())}")
+
+
+def test_mtp_verify_ex_every_mode(sampler, oracle):
+    """Every (model mode, n-gram mode, delta correction) combination, mixed
+    sources per position, against the oracle's mtp_accept_count + tail."""
+    import itertools
+
+    import torch
+
+    from ax_sampler import _abi
+
+    for mm, nm, dc in itertools.product((0, 1), (0, 1, 2), (False, True)):
+        rng, t, d, tp, dp = _ex_case(100 + mm * 10 + nm * 2 + int(dc), B=8)
+        B, D1, V = t.shape
+        D = D1 - 1
+        dids = _draft_ids(oracle, d, DTYPE_F32, B, D, V, dp, 63)
+        src = rng.choice(np.array([1, 2, 3, 4], np.uint32), (B, D))
+        am = np.array([[oracle.argmax_f32(t[b, i]) for i in range(D)] for b in range(B)], np.uint32)
+        ng = src == 3
+        dids = np.where(ng & (rng.random((B, D)) < 0.6), am, np.where(ng, rng.integers(0, V, (B, D)), dids)
+                        ).astype(np.uint32)
+        opts = {"sources": src, "model_mode": mm, "ngram_mode": nm, "delta_correction": dc}
+        us = rng.random((B, D + 1)).astype(np.float32)
+        res = sampler.mtp_verify(_to_dev(t, DTYPE_F32), _to_dev(d, DTYPE_F32), dids, tp, dp, uniforms=us,
+                                 options=opts)
+        torch.cuda.synchronize()
+        g_ids, g_n, g_ac, g_fl = res.numpy()
+        for b in range(B):
+            if g_fl[b] & np.uint32(_abi.MTP_FLAG_NEAR_ACCEPT):
+                continue
+            ob = {k: (v[b] if isinstance(v, np.ndarray) else v) for k, v in opts.items()}
+            want, ac = _mtp_expect(oracle, t[b], d[b], dids[b], tp[b:b + 1], dp[b:b + 1], us[b], ob, D)
+            assert g_ids[b, : g_n[b]].tolist() == want and g_ac[b] == ac, (mm, nm, dc, b)
+    log("mtp_verify_ex: all 12 mode combinations match")
