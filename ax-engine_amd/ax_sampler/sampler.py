@@ -115,6 +115,19 @@ def _csr(rows: Sequence[Sequence[int]]) -> Tuple[np.ndarray, np.ndarray]:
     return flat, off
 
 
+class PreparedSample:
+    """One sampling step's descriptor and outputs (HipSampler.prepare_sample)."""
+
+    def __init__(self, sampler: "HipSampler", desc, outputs, result: SampleResult):
+        self.sampler, self.desc, self.outputs, self.result = sampler, desc, outputs, result
+        self._dp, self._op = C.byref(desc), C.byref(outputs)
+
+    def run(self, stream=None) -> SampleResult:
+        s = self.sampler
+        _abi.check(s.L.axs_sample_batch(s.ctx, self._dp, self._op, s._stream(stream)))
+        return self.result
+
+
 class HipSampler:
     """A sampler context on one GPU (``axs_context``): device workspace for up
     to ``max_batch`` rows of ``max_vocab`` ids."""
@@ -178,6 +191,16 @@ class HipSampler:
         stream=None,
     ) -> SampleResult:
         """One batched sampling step over device logits [B, V] / [B, 1, V]."""
+        prep = self.prepare_sample(logits, params, history=history, mask_words=mask_words, bias=bias,
+                                   uniforms=uniforms, logprobs=logprobs, kept_cap=kept_cap)
+        prep.run(stream)
+        return prep.result
+
+    def prepare_sample(self, logits, params, *, history=None, mask_words=None, bias=None, uniforms=None,
+                       logprobs: bool = False, kept_cap: int = 0) -> "PreparedSample":
+        """The descriptor and output buffers of one sampling step, built once:
+        ``run()`` then enqueues the step with a single C-ABI call and no
+        allocation (for loops that sample the same buffers every step)."""
         torch = _torch()
         if logits.dim() == 3:
             if logits.shape[1] != 1:
@@ -253,8 +276,7 @@ class HipSampler:
         o.kept_ids = _ptr(kept)
         o.kept_count = _ptr(kept_n)
         o.kept_cap = kept_cap
-        _abi.check(self.L.axs_sample_batch(self.ctx, C.byref(d), C.byref(o), self._stream(stream)))
-        return SampleResult(out_ids, out_lp, out_flags, kept, kept_n, tuple(keep))
+        return PreparedSample(self, d, o, SampleResult(out_ids, out_lp, out_flags, kept, kept_n, tuple(keep)))
 
     def sample_host(
         self,

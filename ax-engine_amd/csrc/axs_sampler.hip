@@ -3605,8 +3605,8 @@ struct axs_context {
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev[AXS_KERNEL_COUNT];
     // Calls are serialised: the lock covers each call's enqueue, and a call
     // on another stream than the previous one first waits for the previous
-    // call's work (done_ev), so two streams never run on the workspace at
-    // once.
+    // stream's work (done_ev recorded there), so two streams never run on
+    // the workspace at once.
     std::mutex mu;
     hipEvent_t done_ev;
     hipStream_t last_stream;
@@ -3886,23 +3886,22 @@ int run_pipeline(axs_context* c, KArgs& a, const Plan& pl, hipStream_t s) {
 }
 
 // A call's work on stream s follows the previous call's when that ran on
-// another stream (not while s is being captured into a graph: the previous
-// call's event is then outside the capture).
+// another stream: an event recorded on the previous stream now (after its
+// enqueued work) and waited for on s.  Consecutive calls on one stream cost
+// nothing here.  A stream being captured into a graph is not recorded as the
+// previous stream (its work runs at replay).
 int order_begin(axs_context* c, hipStream_t s) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    AXS_HIP_CHECK(hipStreamIsCapturing(s, &cs));
-    if (c->has_last && c->last_stream != s && cs == hipStreamCaptureStatusNone)
-        AXS_HIP_CHECK(hipStreamWaitEvent(s, c->done_ev, 0));
+    if (c->has_last && c->last_stream != s) {
+        hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+        AXS_HIP_CHECK(hipStreamIsCapturing(c->last_stream, &cs));
+        if (cs == hipStreamCaptureStatusNone) {
+            AXS_HIP_CHECK(hipEventRecord(c->done_ev, c->last_stream));
+            AXS_HIP_CHECK(hipStreamWaitEvent(s, c->done_ev, 0));
+        }
+    }
     return AXS_OK;
 }
 int order_end(axs_context* c, hipStream_t s) {
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    AXS_HIP_CHECK(hipStreamIsCapturing(s, &cs));
-    if (cs != hipStreamCaptureStatusNone) {
-        c->has_last = false;
-        return AXS_OK;
-    }
-    AXS_HIP_CHECK(hipEventRecord(c->done_ev, s));
     c->last_stream = s;
     c->has_last = true;
     return AXS_OK;

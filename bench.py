@@ -250,8 +250,14 @@ def main():
                 torch.from_numpy(w.bias_off).to(dev)) if w.bias_ids is not None else None
         params = torch.from_numpy(w.params.view(np.uint8)).to(dev)
 
+        # one prepared descriptor per input set: a step is one C-ABI call
+        preps = [s.prepare_sample(x, params, history=hist, mask_words=mask, bias=bias) for x in sets]
+        sptr = s._stream(stream)
+
         def step(i):
-            return s.sample(sets[i % len(sets)], params, history=hist, mask_words=mask, bias=bias)
+            p = preps[i % len(preps)]
+            _abi.check(s.L.axs_sample_batch(s.ctx, p._dp, p._op, sptr))
+            return p.result
 
         rows_per_step = w.B
         alg = w.algorithmic_bytes()

@@ -21,9 +21,11 @@
  *   - No torch or HIP types appear in the signatures.
  *   - A context may be shared by threads: its calls are serialised (a lock
  *     around each call's enqueue), and a call on another stream than the
- *     previous call's first waits for that call's work (an event), so the
- *     context's workspace is never used by two streams at once.  One context
- *     per thread avoids the waiting.
+ *     previous call's first waits for the work enqueued on that stream (an
+ *     event recorded there), so the context's workspace is never used by two
+ *     streams at once; that previous stream must still exist.  Consecutive
+ *     calls on one stream add no event.  One context per thread avoids the
+ *     waiting.
  */
 #ifndef AX_HIP_SAMPLER_H
 #define AX_HIP_SAMPLER_H
