@@ -1828,6 +1828,8 @@ struct ExLds {
     uint32_t cnt[NBUCKET];  // bucket counts, then bucket ends; then sort scratch
     uint64_t stage[(NT_EX / 64) * 128];  // each wave's window of keys
     uint32_t mixed[NMIXW];  // buckets of more than 64 keys with two different p
+    uint32_t topv[NMIXW];   // tail buckets holding their top value
+    uint32_t done[NMIXW];   // tail buckets sorted and summed element by element
     Xd w[NT_EX / 64];
     uint32_t u[NT_EX / 64];
     float s;
@@ -2623,6 +2625,9 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     }
     const bool xminp = xs.mode == M_MINP;
     const bool xsorted = xs.sorted != 0;
+    // sorted laws keep only p >= pmin: below ln(min(pmin, min_p)) - 0.7 the
+    // exp is under half of both (no key, and no min-p boundary), so it is skipped
+    const double xskip = xsorted ? log((double)(xminp ? fminf(xs.pmin, c.p.min_p) : xs.pmin)) - 0.7 : -INFINITY;
     const bool hok = !(SL.err & RERR_HASH);
     float* dense = a.dense + (size_t)r * a.vocab;
     uint64_t* ck = a.ckey + (size_t)r * a.vocab;
@@ -2662,10 +2667,10 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             for (int q = 0; q < EPV; ++q) {
                 const uint32_t e = e0 + (uint32_t)q;
                 if ((sk >> q) & 1u) v[q] = xval(e, unpack<DT>(T.raw[j], q), MASK && !((mw >> (e & 31u)) & 1u));
-                const float pr = prob_of(v[q], xs.m, xs.inv);
+                const float pr = prob_of_above(v[q], xs.m, xs.inv, xskip);
                 bool keep = true;
                 if (xminp) {
-                    if (!isnan(v[q]) && e < hi) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
+                    if (!isnan(v[q]) && e < hi && pr > 0.0f) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
                     keep = pr >= c.p.min_p;
                 }
                 v[q] = keep ? pr : 0.0f;
@@ -2742,13 +2747,16 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
         float mg = INFINITY;
         uint32_t cnt = 0;
         float* dense = a.dense + (size_t)r * a.vocab;
+        // sorted laws keep only p >= pmin: below ln(min(pmin, min_p)) - 0.7 the
+        // exp is under half of both (no key, and no min-p boundary), so it is skipped
+        const double skip = rs.sorted ? log((double)(minp ? fminf(rs.pmin, minp_v) : rs.pmin)) - 0.7 : -INFINITY;
         // pass 1: exact probabilities; dense rows are written here, sorted rows
         // only counted
         auto pass1 = [&](uint32_t e, float l) {
-            float pr = prob_of(l, rs.m, rs.inv);
+            float pr = prob_of_above(l, rs.m, rs.inv, skip);
             bool keep = true;
             if (minp) {
-                if (!isnan(l)) mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
+                if (!isnan(l) && pr > 0.0f) mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
                 keep = pr >= minp_v;
             }
             float v = keep ? pr : 0.0f;
@@ -2769,7 +2777,7 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
             uint32_t o = 0;
             // pass 2: write the compacted (p desc, id asc) keys
             auto pass2 = [&](uint32_t e, float l) {
-                float pr = prob_of(l, rs.m, rs.inv);
+                float pr = prob_of_above(l, rs.m, rs.inv, skip);
                 if (minp && !(pr >= minp_v)) pr = 0.0f;
                 if (pr >= rs.pmin) dst[o++] = key_pdesc(pr, e);
             };
@@ -2865,6 +2873,21 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t key) {
     return b < NBUCKET ? b : NBUCKET - 1;
 }
 
+// Buckets of p >= 2^-14 (bucket 7168 holds 2^-14 itself) are the head:
+// sorted and summed element by element.  The tail buckets [NHB, TB_END)
+// (2^-24 <= p < 2^-14) hold one binade each except for a power-of-two top
+// value.  Once the running sum is >= 1 (after the maximum, p = 1) its
+// spacing U is >= 2^-23 and a tail term x has x / U = M / 2^d with M its
+// significand and d >= 15, so the rounding boundaries of x / U fall on
+// multiples of 2^14 of the bit pattern: every element below the bucket's top
+// value adds the same number of units, in any order.  Such a bucket is one
+// term (count x units) while the sum stays in its binade; a bucket that
+// would leave the binade or that holds its top value is sorted and summed
+// element by element.
+constexpr uint32_t NHB = 7169;
+constexpr uint32_t TB_END = 12289;  // bucket of 2^-24, the lowest floor, + 1
+__device__ __forceinline__ uint32_t bucket_top(uint32_t b) { return 0x3F800000u - (b << 14); }
+
 // Row r's exact path (rs: its state; X: LDS scratch).  Called by the NT_EX
 // threads of one workgroup; XI = keys or terms per thread in flight at once
 // (a register budget).
@@ -2887,26 +2910,106 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     const float* dense = a.dense + (size_t)r * V;
     float* S = a.sbuf + (size_t)r * V;
     if (tid == 0) s_err = 0;
-    // block sort of keys[st, en) by (p desc, id asc): in LDS (s_cnt) up to
+    uint64_t* const ck2 = keys;  // bucket-grouped keys; unsorted tail buckets stay here
+    // block sort of kp[st, en) by (p desc, id asc): in LDS (s_cnt) up to
     // BIG_LDS_SORT keys, else in the row's HBM scratch.  Uniform control flow.
-    auto sort_range = [&](uint32_t st, uint32_t en) {
+    auto sort_range_in = [&](uint64_t* kp, uint32_t st, uint32_t en) {
         const uint32_t mcount = en - st;
         if (mcount <= 1) return;
         const uint32_t np2 = next_pow2(mcount);
         uint64_t* t = np2 <= BIG_LDS_SORT ? (uint64_t*)s_cnt : a.tmp64 + (size_t)r * a.tmp_stride;
-        for (uint32_t i = tid; i < np2; i += NT_EX) t[i] = i < mcount ? keys[st + i] : 0ull;
+        for (uint32_t i = tid; i < np2; i += NT_EX) t[i] = i < mcount ? kp[st + i] : 0ull;
         __threadfence_block();
         __syncthreads();
         block_sort_desc<NT_EX>(t, np2);
-        for (uint32_t i = tid; i < mcount; i += NT_EX) keys[st + i] = t[i];
+        for (uint32_t i = tid; i < mcount; i += NT_EX) kp[st + i] = t[i];
         __threadfence_block();
         __syncthreads();
     };
+    auto sort_range = [&](uint32_t st, uint32_t en) { sort_range_in(keys, st, en); };
+    // Each bucket of at most 64 keys among positions [p0, p1) of the grouped
+    // keys gk is sorted by the wave whose window of 64 positions holds its
+    // start: the window's 128 keys staged in LDS, each key's rank = the keys
+    // of its bucket above it, written to dk.  Keys of larger buckets are
+    // copied in place, and a large bucket holding two different p is marked
+    // for a block sort; one whose p are all equal is already in p order, and
+    // its ids are ordered later only where an output reads them.  Bucket
+    // ends in s_cnt.
+    auto window_sort = [&](const uint64_t* gk, uint64_t* dk, uint32_t p0, uint32_t p1) {
+        const int wv = tid >> 6, lane = tid & 63;
+        uint64_t* st = XL.stage + (uint32_t)wv * 128u;
+        constexpr uint32_t WSTEP = 64u * (NT_EX / 64);
+        auto wload = [&](uint32_t at) { return at < p1 ? gk[at] : 0ull; };
+        uint64_t n0 = wload(p0 + (uint32_t)wv * 64u + lane), n1 = wload(p0 + (uint32_t)wv * 64u + 64u + lane);
+        for (uint32_t s0 = p0 + (uint32_t)wv * 64u; s0 < p1; s0 += WSTEP) {
+            const uint64_t k0 = n0, k1 = n1;
+            n0 = wload(s0 + WSTEP + lane);  // the next window's keys, in flight meanwhile
+            n1 = wload(s0 + WSTEP + 64u + lane);
+            st[lane] = k0;
+            st[64 + lane] = k1;
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+#pragma unroll
+            for (int h = 0; h < 2; ++h) {
+                const uint32_t pos = s0 + (uint32_t)h * 64u + (uint32_t)lane;
+                const uint64_t key = h ? k1 : k0;
+                if (pos >= p1) continue;
+                const uint32_t b = bucket_of(key);
+                const uint32_t bs = b ? s_cnt[b - 1] : 0u, be = s_cnt[b];
+                if (be - bs <= 64u) {
+                    if (bs >= s0 && bs < s0 + 64u) {
+                        uint32_t rank = 0, q = bs;
+                        for (; q + 4u <= be; q += 4u) {  // four LDS reads in flight
+                            const uint64_t c0 = st[q - s0], c1 = st[q + 1u - s0];
+                            const uint64_t c2 = st[q + 2u - s0], c3 = st[q + 3u - s0];
+                            rank += (c0 > key ? 1u : 0u) + (c1 > key ? 1u : 0u) + (c2 > key ? 1u : 0u) +
+                                    (c3 > key ? 1u : 0u);
+                        }
+                        for (; q < be; ++q) rank += st[q - s0] > key ? 1u : 0u;
+                        dk[bs + rank] = key;
+                    }
+                } else {
+                    if (h == 0) dk[pos] = key;
+                    if (pdesc_p(key) != pdesc_p(gk[bs])) atomicOr(&XL.mixed[b >> 5], 1u << (b & 31u));
+                }
+            }
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        }
+        __threadfence_block();
+        __syncthreads();
+    };
+    // large buckets with two different p (marked in XL.mixed): block sorts of
+    // keys (uniform loop)
+    auto mixed_sorts = [&]() {
+        uint32_t anym = 0;
+        for (uint32_t i = tid; i < NMIXW; i += NT_EX) anym |= XL.mixed[i];
+        if (__syncthreads_or(anym != 0u))
+        for (uint32_t wi = 0; wi < NMIXW; ++wi) {
+            uint32_t bits = XL.mixed[wi];
+            while (bits) {
+                const uint32_t b = wi * 32u + (uint32_t)__ffs((int)bits) - 1u;
+                bits &= bits - 1u;
+                sort_range(b ? bend[b - 1] : 0u, bend[b]);
+            }
+        }
+        __syncthreads();
+    };
 
+    // positions [0, n_head) are sorted in keys and summed element by element;
+    // the tail buckets' keys stay grouped in ck2 unless tail_all
+    uint32_t n_head = n;
+    bool tail_all = true;
     if (sorted) {
         // counting sort by p bucket (descending p) into keys
         for (uint32_t i = tid; i < NBUCKET; i += NT_EX) s_cnt[i] = 0;
-        for (uint32_t i = tid; i < NMIXW; i += NT_EX) XL.mixed[i] = 0;
+        for (uint32_t i = tid; i < NMIXW; i += NT_EX) {
+            XL.mixed[i] = 0;
+            XL.topv[i] = 0;
+            XL.done[i] = 0;
+        }
         __syncthreads();
         constexpr uint32_t U = XI;  // keys per thread per round, every load issued first
         for (uint32_t i0 = tid; i0 < n; i0 += NT_EX * U) {
@@ -2915,7 +3018,12 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             for (uint32_t u = 0; u < U; ++u) kk[u] = i0 + u * NT_EX < n ? src[i0 + u * NT_EX] : 0ull;
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u)
-                if (i0 + u * NT_EX < n) atomicAdd(&s_cnt[bucket_of(kk[u])], 1u);
+                if (i0 + u * NT_EX < n) {
+                    const uint32_t b = bucket_of(kk[u]);
+                    atomicAdd(&s_cnt[b], 1u);
+                    if (b >= NHB && (uint32_t)(kk[u] >> 32) == bucket_top(b))
+                        atomicOr(&XL.topv[b >> 5], 1u << (b & 31u));
+                }
         }
         __syncthreads();
         constexpr uint32_t PER = NBUCKET / NT_EX;
@@ -2942,143 +3050,219 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         // s_cnt[b] is now the end of bucket b; kept in HBM for the phases
         // that reuse s_cnt as sort scratch
         for (uint32_t i = tid; i < NBUCKET; i += NT_EX) bend[i] = s_cnt[i];
-        // Each bucket of at most 64 keys is sorted by the wave whose window
-        // of 64 positions holds its start: the window's 128 keys staged in
-        // LDS, each key's rank = the keys of its bucket above it, written to
-        // sorted (the compaction array, free now).  Keys of larger buckets are
-        // copied in place, and a large bucket holding two different p is
-        // marked for a block sort; one whose p are all equal is already in p
-        // order, and its ids are ordered later only where an output reads
-        // them.
-        const int wv = tid >> 6, lane = tid & 63;
-        uint64_t* st = XL.stage + (uint32_t)wv * 128u;
-        constexpr uint32_t WSTEP = 64u * (NT_EX / 64);
-        auto wload = [&](uint32_t at) { return at < n ? keys[at] : 0ull; };
-        uint64_t n0 = wload((uint32_t)wv * 64u + lane), n1 = wload((uint32_t)wv * 64u + 64u + lane);
-        for (uint32_t s0 = (uint32_t)wv * 64u; s0 < n; s0 += WSTEP) {
-            const uint64_t k0 = n0, k1 = n1;
-            n0 = wload(s0 + WSTEP + lane);  // the next window's keys, in flight meanwhile
-            n1 = wload(s0 + WSTEP + 64u + lane);
-            st[lane] = k0;
-            st[64 + lane] = k1;
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-#pragma unroll
-            for (int h = 0; h < 2; ++h) {
-                const uint32_t pos = s0 + (uint32_t)h * 64u + (uint32_t)lane;
-                const uint64_t key = h ? k1 : k0;
-                if (pos >= n) continue;
-                const uint32_t b = bucket_of(key);
-                const uint32_t bs = b ? s_cnt[b - 1] : 0u, be = s_cnt[b];
-                if (be - bs <= 64u) {
-                    if (bs >= s0 && bs < s0 + 64u) {
-                        uint32_t rank = 0, q = bs;
-                        for (; q + 4u <= be; q += 4u) {  // four LDS reads in flight
-                            const uint64_t c0 = st[q - s0], c1 = st[q + 1u - s0];
-                            const uint64_t c2 = st[q + 2u - s0], c3 = st[q + 3u - s0];
-                            rank += (c0 > key ? 1u : 0u) + (c1 > key ? 1u : 0u) + (c2 > key ? 1u : 0u) +
-                                    (c3 > key ? 1u : 0u);
-                        }
-                        for (; q < be; ++q) rank += st[q - s0] > key ? 1u : 0u;
-                        sorted_keys[bs + rank] = key;
-                    }
-                } else {
-                    if (h == 0) sorted_keys[pos] = key;
-                    if (pdesc_p(key) != pdesc_p(keys[bs])) atomicOr(&XL.mixed[b >> 5], 1u << (b & 31u));
-                }
-            }
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        }
-        __threadfence_block();
-        __syncthreads();
+        n_head = s_cnt[NHB - 1];
+        tail_all = n_head >= n;
+        window_sort(keys, sorted_keys, 0u, n_head);
         keys = sorted_keys;
-        // large buckets with two different p: block sorts (uniform loop)
-        uint32_t anym = 0;
-        for (uint32_t i = tid; i < NMIXW; i += NT_EX) anym |= XL.mixed[i];
-        if (__syncthreads_or(anym != 0u))
-        for (uint32_t wi = 0; wi < NMIXW; ++wi) {
-            uint32_t bits = XL.mixed[wi];
-            while (bits) {
-                const uint32_t b = wi * 32u + (uint32_t)__ffs((int)bits) - 1u;
-                bits &= bits - 1u;
-                sort_range(b ? bend[b - 1] : 0u, bend[b]);
-            }
-        }
+        mixed_sorts();
     }
     __syncthreads();
 
-    // exact running sums S[k] = fl(S[k-1] + x_k), in parallel (axs_exact_sum.h)
-    auto X = [&](uint32_t i) -> float { return sorted ? pdesc_p(keys[i]) : dense[i]; };
-    if (tid == 0) {
-        s_s = 0.0f;
-        s_k = 0;
-    }
-    __syncthreads();
+    // exact running sums S[k] = fl(S[k-1] + x_k), in parallel (axs_exact_sum.h),
+    // over positions [k0, kend) of the terms pdesc_p(kp[k]) (dense[k] without
+    // kp) from the sum s0; returns the last sum.  Whole block.
     // Each round: a tile of IT terms per thread, all in the binade of the
     // current sum; the first term that would leave it (the earliest crossing
     // over the block) is added directly by its thread, which sets the next
     // round's start.  The round's state stays in LDS.
     // The round's barriers are LDS-only: S is read only after the loop.
     constexpr uint32_t IT = XI;
-    if (tid == 0) s_cross = NONE;
-    while (true) {
-        const float s = s_s;
-        const uint32_t k = s_k;
-        if (k >= n) break;
-        const Binade bd = binade_of(s);
-        const uint32_t tile = min((uint32_t)NT_EX * IT, n - k);
-        const uint32_t i0 = k + (uint32_t)tid * IT;
-        float xv[IT];
-        Term t[IT];
-        Xd mine = xd_identity();
+    auto elem_sums = [&](const uint64_t* kp, uint32_t k0, uint32_t kend, float s0) -> float {
+        auto X = [&](uint32_t i) -> float { return kp ? pdesc_p(kp[i]) : dense[i]; };
+        if (tid == 0) {
+            s_s = s0;
+            s_k = k0;
+            s_cross = NONE;
+        }
+        __syncthreads();
+        while (true) {
+            const float s = s_s;
+            const uint32_t k = s_k;
+            if (k >= kend) break;
+            const Binade bd = binade_of(s);
+            const uint32_t tile = min((uint32_t)NT_EX * IT, kend - k);
+            const uint32_t i0 = k + (uint32_t)tid * IT;
+            float xv[IT];
+            Term t[IT];
+            Xd mine = xd_identity();
 #pragma unroll
-        for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
+            for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
 #pragma unroll
-        for (uint32_t j = 0; j < IT; ++j) {
-            if (i0 + j < k + tile) {
-                t[j] = term_of(xv[j], bd.E);
-                mine = xd_compose(mine, xd_of(t[j]));
+            for (uint32_t j = 0; j < IT; ++j) {
+                if (i0 + j < k + tile) {
+                    t[j] = term_of(xv[j], bd.E);
+                    mine = xd_compose(mine, xd_of(t[j]));
+                }
+            }
+            Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
+            const uint32_t b0 = bd.A & 1u;
+            uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
+            uint32_t par = b0 ? pre.par1 : pre.par0;
+            uint32_t mycross = NONE;
+            float xs = 0.0f, last = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) {
+                const uint32_t i = i0 + j;
+                if (i >= k + tile || mycross != NONE) continue;
+                const uint32_t cc = par ? t[j].c1 : t[j].c0;
+                if (acc + cc >= (1ull << 24)) {
+                    mycross = i;
+                    xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
+                    continue;
+                }
+                acc += cc;
+                par = (uint32_t)(acc & 1u);
+                last = binade_value((uint32_t)acc, bd.E);
+                S[i] = last;
+            }
+            if (mycross != NONE) atomicMin(&s_cross, mycross);
+            lds_barrier();
+            const uint32_t kc = s_cross;
+            if (kc == NONE) {
+                if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last term
+                    s_s = last;
+                    s_k = k + tile;
+                }
+            } else if (mycross == kc) {
+                S[kc] = xs;
+                s_s = xs;
+                s_k = kc + 1u;
+            }
+            lds_barrier();
+            if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
+        }
+        __threadfence_block();
+        __syncthreads();
+        const float fin = s_s;
+        __syncthreads();
+        return fin;
+    };
+    // tail bucket b sorted in ck2 and summed element by element from the sum
+    // before it (whole block, once per bucket)
+    auto bucket_elems = [&](uint32_t b, float sb) -> float {
+        const uint32_t bs = bend[b - 1], be = bend[b];
+        sort_range_in(ck2, bs, be);
+        const float se = elem_sums(ck2, bs, be, sb);
+        if (tid == 0) XL.done[b >> 5] |= 1u << (b & 31u);
+        __syncthreads();
+        return se;
+    };
+    // The tail buckets [NHB, TB_END) from the sum s0 (>= 1): a round takes IT
+    // buckets per thread as terms of count x units; the first bucket that
+    // would leave the binade, or that holds its top value, is sorted and
+    // summed element by element, and the next round starts after it.  S is
+    // written at each bucket's last position.
+    auto tail_sums = [&](float s0) {
+        if (tid == 0) {
+            s_s = s0;
+            s_k = NHB;
+            s_cross = NONE;
+        }
+        __syncthreads();
+        while (true) {
+            const float s = s_s;
+            const uint32_t k = s_k;
+            if (k >= TB_END) break;
+            const Binade bd = binade_of(s);
+            const uint32_t tile = min((uint32_t)NT_EX * IT, TB_END - k);
+            const uint32_t i0 = k + (uint32_t)tid * IT;
+            uint64_t inc[IT];
+            uint32_t be[IT];
+            uint32_t evm = 0, nem = 0;  // bit j: bucket i0 + j is an event / not empty
+            uint32_t prev = i0 < k + tile ? bend[i0 - 1u] : 0u;
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) be[j] = i0 + j < k + tile ? bend[i0 + j] : 0u;
+            uint64_t tot = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) {
+                const uint32_t b = i0 + j;
+                inc[j] = 0;
+                if (b < k + tile) {
+                    const uint32_t cnt = be[j] - prev;
+                    prev = be[j];
+                    if (cnt) {
+                        nem |= 1u << j;
+                        const Term t = term_of(bits_f32(bucket_top(b) - 1u), bd.E);
+                        if (((XL.topv[b >> 5] >> (b & 31u)) & 1u) || t.c0 != t.c1) evm |= 1u << j;
+                        else inc[j] = (uint64_t)cnt * t.c0;
+                    }
+                    tot += inc[j];
+                }
+            }
+            // every term adds the same for either parity: a plain sum scan
+            Xd mine = xd_identity();
+            mine.inc0 = mine.inc1 = tot;
+            mine.par0 = (uint32_t)(tot & 1u);
+            mine.par1 = (uint32_t)((tot + 1u) & 1u);
+            const Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
+            uint64_t acc = (uint64_t)bd.A + pre.inc0;
+            uint32_t mystop = NONE;
+            float stopv = 0.0f, last = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) {
+                const uint32_t b = i0 + j;
+                if (b >= k + tile || mystop != NONE) continue;
+                if (((evm >> j) & 1u) || acc + inc[j] >= (1ull << 24)) {
+                    mystop = b;
+                    stopv = binade_value((uint32_t)acc, bd.E);
+                    continue;
+                }
+                acc += inc[j];
+                last = binade_value((uint32_t)acc, bd.E);
+                if ((nem >> j) & 1u) S[be[j] - 1u] = last;
+            }
+            if (mystop != NONE) atomicMin(&s_cross, mystop);
+            lds_barrier();
+            const uint32_t kc = s_cross;
+            if (kc == NONE) {
+                if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last bucket
+                    s_s = last;
+                    s_k = k + tile;
+                }
+            } else if (mystop == kc) {
+                s_s = stopv;
+                s_k = kc;
+            }
+            lds_barrier();
+            if (kc != NONE) {
+                const float sb = s_s;
+                __syncthreads();  // s_s read by every thread before the bucket's sums reset it
+                const float se = bucket_elems(kc, sb);
+                if (tid == 0) {
+                    s_s = se;
+                    s_k = kc + 1u;
+                    s_cross = NONE;
+                }
+                __syncthreads();
+            } else if (tid == 0) {
+                s_cross = NONE;  // read by every thread before the barrier above
             }
         }
-        Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
-        const uint32_t b0 = bd.A & 1u;
-        uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
-        uint32_t par = b0 ? pre.par1 : pre.par0;
-        uint32_t mycross = NONE;
-        float xs = 0.0f, last = 0.0f;
-#pragma unroll
-        for (uint32_t j = 0; j < IT; ++j) {
-            const uint32_t i = i0 + j;
-            if (i >= k + tile || mycross != NONE) continue;
-            const uint32_t cc = par ? t[j].c1 : t[j].c0;
-            if (acc + cc >= (1ull << 24)) {
-                mycross = i;
-                xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
-                continue;
+        __threadfence_block();
+        __syncthreads();
+    };
+    // the whole tail sorted into keys after the head, as the head is
+    auto tail_sort_all = [&]() {
+        for (uint32_t i = tid; i < NBUCKET; i += NT_EX) s_cnt[i] = bend[i];
+        for (uint32_t i = tid; i < NMIXW; i += NT_EX) XL.mixed[i] = 0;
+        __syncthreads();
+        window_sort(ck2, keys, n_head, n);
+        mixed_sorts();
+        tail_all = true;
+    };
+    if (!sorted) {
+        elem_sums(nullptr, 0u, V, 0.0f);
+    } else if (n > 0) {
+        const float sh = elem_sums(keys, 0u, n_head, 0.0f);
+        if (!tail_all) {
+            if (sh >= 1.0f) {
+                tail_sums(sh);
+            } else {  // not reached: the head holds the maximum (p = 1)
+                tail_sort_all();
+                elem_sums(keys, n_head, n, sh);
+                n_head = n;
             }
-            acc += cc;
-            par = (uint32_t)(acc & 1u);
-            last = binade_value((uint32_t)acc, bd.E);
-            S[i] = last;
         }
-        if (mycross != NONE) atomicMin(&s_cross, mycross);
-        lds_barrier();
-        const uint32_t kc = s_cross;
-        if (kc == NONE) {
-            if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last term
-                s_s = last;
-                s_k = k + tile;
-            }
-        } else if (mycross == kc) {
-            S[kc] = xs;
-            s_s = xs;
-            s_k = kc + 1u;
-        }
-        lds_barrier();
-        if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
     }
     __threadfence_block();
     __syncthreads();  // every S store complete before the decisions read S
@@ -3180,16 +3364,63 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         }
         return;
     }
+    // Sorted rows: positions >= n_head lie in tail buckets, whose sums are
+    // exact at each bucket's last position; a bucket that a decision reads
+    // inside is sorted and summed element by element first (whole block:
+    // every thread makes the same calls).
+    auto tail_bucket_at = [&](uint32_t i) -> uint32_t {  // first b with bend[b] > i
+        uint32_t lo = NHB, hi = TB_END - 1u;
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            if (bend[mid] > i) hi = mid;
+            else lo = mid + 1;
+        }
+        return lo;
+    };
+    auto ensure_bucket = [&](uint32_t b) {
+        if ((XL.done[b >> 5] >> (b & 31u)) & 1u) return;
+        const float sb = S[bend[b - 1] - 1u];
+        __syncthreads();
+        bucket_elems(b, sb);
+    };
+    auto S_at = [&](uint32_t i) -> float {
+        if (i >= n_head) {
+            const uint32_t b = tail_bucket_at(i);
+            if (i + 1u != bend[b]) ensure_bucket(b);
+        }
+        return S[i];
+    };
+    auto key_at = [&](uint32_t i) -> uint64_t {
+        if (i < n_head || tail_all) return keys[i];
+        ensure_bucket(tail_bucket_at(i));
+        return ck2[i];
+    };
+    // first position in [0, lim) with S >= t, lim if none
+    auto locate = [&](float t, uint32_t lim) -> uint32_t {
+        const uint32_t hl = lim < n_head ? lim : n_head;
+        const uint32_t j = first_ge(S, 0, hl, t);
+        if (j < hl || lim <= n_head) return j;
+        uint32_t lo = NHB, hi = TB_END;  // the first tail bucket whose sum reaches t
+        while (lo < hi) {
+            const uint32_t mid = lo + (hi - lo) / 2;
+            if (S[bend[mid] - 1u] >= t) hi = mid;
+            else lo = mid + 1;
+        }
+        if (lo >= TB_END || bend[lo - 1] >= lim) return lim;
+        ensure_bucket(lo);
+        const uint32_t jj = first_ge(S, bend[lo - 1], bend[lo], t);
+        return jj < lim ? jj : lim;
+    };
     if (sorted) {
         const uint32_t L = n;
         uint32_t nk = L;
         if (topp_active(p)) {
-            float total = S[L - 1];
+            float total = S[L - 1];  // the last bucket's end
             float cutoff = __fmul_rn(p.top_p, total);
-            uint32_t j = first_ge(S, 0, L, cutoff);
+            uint32_t j = locate(cutoff, L);
             nk = j < L ? j + 1 : L;
-            double up = (double)S[nk - 1] - (double)cutoff;
-            double lo = nk >= 2 ? (double)cutoff - (double)S[nk - 2] : INFINITY;
+            double up = (double)S_at(nk - 1) - (double)cutoff;
+            double lo = nk >= 2 ? (double)cutoff - (double)S_at(nk - 2) : INFINITY;
             if (fmin(up, lo) / (double)total < 1e-6 && (p.top_k == 0 || nk <= p.top_k))
                 flags |= AXS_FLAG_NEAR_NUCLEUS;
             kept = nk;
@@ -3200,15 +3431,15 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         if (p.top_k > 0 && kept > p.top_k) kept = p.top_k;
         Lk = kept < L ? kept : L;
         if (kept < L) {
-            float pa = pdesc_p(keys[kept - 1]), pb = pdesc_p(keys[kept]);
+            float pa = pdesc_p(key_at(kept - 1)), pb = pdesc_p(key_at(kept));
             if (pa != pb && (double)pa - (double)pb <= 2.0 * ulp_f(pa)) flags |= AXS_FLAG_NEAR_TIE;
         }
-        F = S[Lk - 1];
+        F = S_at(Lk - 1);
         const float thr = __fmul_rn(rs.u, F);
-        uint32_t j = first_ge(S, 0, Lk, thr);
+        uint32_t j = locate(thr, Lk);
         if (j >= Lk) j = Lk - 1;  // unreachable: S[Lk-1] = F >= u*F
-        double up = (double)S[j] - (double)thr;
-        double lo = j > 0 ? (double)thr - (double)S[j - 1] : INFINITY;
+        double up = (double)S_at(j) - (double)thr;
+        double lo = j > 0 ? (double)thr - (double)S_at(j - 1) : INFINITY;
         if (fmin(up, lo) / (double)F < 1e-6) flags |= AXS_FLAG_NEAR_DRAW;
         // ids are read at the draw position and in the kept prefixes; a
         // bucket of more than 64 keys with a single p is still in arbitrary
@@ -3216,6 +3447,8 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         const uint32_t po = (a.out_kept && a.out_kept_cap > 0) ? min(Lk, (uint32_t)a.out_kept_cap) : 0u;
         const uint32_t pw = a.ws_kept_id ? min(Lk, KEPT_CAP) : 0u;
         const uint32_t P = max(po, pw);
+        const uint64_t kj0 = key_at(j);  // a tail bucket read here is sorted in ck2
+        if (P > n_head && !tail_all) tail_sort_all();
         auto order_ids = [&](uint32_t pos) -> uint32_t {  // returns the end of pos's bucket
             const uint32_t b = bucket_of(keys[pos]);
             const uint32_t bs = b ? bend[b - 1] : 0u, be = bend[b];
@@ -3223,9 +3456,10 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             return be;
         };
         for (uint32_t pos = 0; pos < P;) pos = order_ids(pos);
-        if (j >= P) order_ids(j);
-        tok = pdesc_id(keys[j]);
-        pj = pdesc_p(keys[j]);
+        if (j >= P && (j < n_head || P > n_head)) order_ids(j);
+        const uint64_t kj = (j < n_head || P > n_head) ? keys[j] : kj0;
+        tok = pdesc_id(kj);
+        pj = pdesc_p(kj);
         if (kept == 0xFFFFFFFFu) kept = L;  // min-p survivors below 2^-24 are not listed
     } else {
         F = S[V - 1];
