@@ -3061,81 +3061,78 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     // exact running sums S[k] = fl(S[k-1] + x_k), in parallel (axs_exact_sum.h),
     // over positions [k0, kend) of the terms pdesc_p(kp[k]) (dense[k] without
     // kp) from the sum s0; returns the last sum.  Whole block.
-    // Each round: a tile of IT terms per thread, all in the binade of the
-    // current sum; the first term that would leave it (the earliest crossing
-    // over the block) is added directly by its thread, which sets the next
-    // round's start.  The round's state stays in LDS.
-    // The round's barriers are LDS-only: S is read only after the loop.
+    // A tile of IT terms per thread is loaded once; a scan adds the terms in
+    // the binade of the current sum, and the first term that would leave it
+    // (the earliest crossing over the block) is added directly by its
+    // thread; the rest of the tile is scanned again in the new binade.  The
+    // barriers are LDS-only: S is read only after the loop.
     constexpr uint32_t IT = XI;
     auto elem_sums = [&](const uint64_t* kp, uint32_t k0, uint32_t kend, float s0) -> float {
         auto X = [&](uint32_t i) -> float { return kp ? pdesc_p(kp[i]) : dense[i]; };
-        if (tid == 0) {
-            s_s = s0;
-            s_k = k0;
-            s_cross = NONE;
-        }
+        if (tid == 0) s_cross = NONE;
         __syncthreads();
-        while (true) {
-            const float s = s_s;
-            const uint32_t k = s_k;
-            if (k >= kend) break;
-            const Binade bd = binade_of(s);
+        float s = s0;
+        for (uint32_t k = k0; k < kend;) {
             const uint32_t tile = min((uint32_t)NT_EX * IT, kend - k);
             const uint32_t i0 = k + (uint32_t)tid * IT;
             float xv[IT];
-            Term t[IT];
-            Xd mine = xd_identity();
 #pragma unroll
             for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
+            uint32_t kk = k;  // the tile's first term not yet added
+            while (true) {
+                const Binade bd = binade_of(s);
+                Term t[IT];
+                Xd mine = xd_identity();
 #pragma unroll
-            for (uint32_t j = 0; j < IT; ++j) {
-                if (i0 + j < k + tile) {
-                    t[j] = term_of(xv[j], bd.E);
-                    mine = xd_compose(mine, xd_of(t[j]));
+                for (uint32_t j = 0; j < IT; ++j) {
+                    t[j].c0 = t[j].c1 = 0u;
+                    if (i0 + j >= kk && i0 + j < k + tile) {
+                        t[j] = term_of(xv[j], bd.E);
+                        mine = xd_compose(mine, xd_of(t[j]));
+                    }
                 }
-            }
-            Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
-            const uint32_t b0 = bd.A & 1u;
-            uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
-            uint32_t par = b0 ? pre.par1 : pre.par0;
-            uint32_t mycross = NONE;
-            float xs = 0.0f, last = 0.0f;
+                Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
+                const uint32_t b0 = bd.A & 1u;
+                uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
+                uint32_t par = b0 ? pre.par1 : pre.par0;
+                uint32_t mycross = NONE;
+                float xs = 0.0f, last = 0.0f;
 #pragma unroll
-            for (uint32_t j = 0; j < IT; ++j) {
-                const uint32_t i = i0 + j;
-                if (i >= k + tile || mycross != NONE) continue;
-                const uint32_t cc = par ? t[j].c1 : t[j].c0;
-                if (acc + cc >= (1ull << 24)) {
-                    mycross = i;
-                    xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
-                    continue;
+                for (uint32_t j = 0; j < IT; ++j) {
+                    const uint32_t i = i0 + j;
+                    if (i < kk || i >= k + tile || mycross != NONE) continue;
+                    const uint32_t cc = par ? t[j].c1 : t[j].c0;
+                    if (acc + cc >= (1ull << 24)) {
+                        mycross = i;
+                        xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
+                        continue;
+                    }
+                    acc += cc;
+                    par = (uint32_t)(acc & 1u);
+                    last = binade_value((uint32_t)acc, bd.E);
+                    S[i] = last;
                 }
-                acc += cc;
-                par = (uint32_t)(acc & 1u);
-                last = binade_value((uint32_t)acc, bd.E);
-                S[i] = last;
-            }
-            if (mycross != NONE) atomicMin(&s_cross, mycross);
-            lds_barrier();
-            const uint32_t kc = s_cross;
-            if (kc == NONE) {
-                if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last term
-                    s_s = last;
-                    s_k = k + tile;
+                if (mycross != NONE) atomicMin(&s_cross, mycross);
+                lds_barrier();
+                const uint32_t kc = s_cross;
+                if (kc == NONE) {
+                    if (k + tile - 1u - i0 < IT) s_s = last;  // this thread holds the tile's last term
+                } else if (mycross == kc) {
+                    S[kc] = xs;
+                    s_s = xs;
                 }
-            } else if (mycross == kc) {
-                S[kc] = xs;
-                s_s = xs;
-                s_k = kc + 1u;
+                lds_barrier();
+                s = s_s;  // rewritten only after the next scan's barriers
+                if (kc == NONE) break;
+                if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
+                kk = kc + 1u;
+                if (kk >= k + tile) break;
             }
-            lds_barrier();
-            if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
+            k += tile;
         }
         __threadfence_block();
         __syncthreads();
-        const float fin = s_s;
-        __syncthreads();
-        return fin;
+        return s;
     };
     // tail bucket b sorted in ck2 and summed element by element from the sum
     // before it (whole block, once per bucket)
@@ -3148,66 +3145,80 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         return se;
     };
     // The tail buckets [NHB, TB_END) from the sum s0 (>= 1): a round takes IT
-    // buckets per thread as terms of count x units; the first bucket that
-    // would leave the binade, or that holds its top value, is sorted and
-    // summed element by element, and the next round starts after it.  S is
-    // written at each bucket's last position.
+    // buckets per thread as terms: the copies of the top value first (their
+    // count read from the bucket's keys; a possible tie makes that term
+    // parity-dependent), then count x units for the rest.  The first bucket
+    // that would leave the binade (or a large bucket holding its top value)
+    // is sorted and summed element by element, and the next round starts
+    // after it.  S is written at each bucket's last position.
     auto tail_sums = [&](float s0) {
-        if (tid == 0) {
-            s_s = s0;
-            s_k = NHB;
-            s_cross = NONE;
-        }
+        if (tid == 0) s_cross = NONE;
         __syncthreads();
-        while (true) {
-            const float s = s_s;
-            const uint32_t k = s_k;
-            if (k >= TB_END) break;
+        float s = s0;
+        for (uint32_t k = NHB; k < TB_END;) {
             const Binade bd = binade_of(s);
             const uint32_t tile = min((uint32_t)NT_EX * IT, TB_END - k);
             const uint32_t i0 = k + (uint32_t)tid * IT;
-            uint64_t inc[IT];
+            Xd bx[IT];
             uint32_t be[IT];
             uint32_t evm = 0, nem = 0;  // bit j: bucket i0 + j is an event / not empty
             uint32_t prev = i0 < k + tile ? bend[i0 - 1u] : 0u;
 #pragma unroll
             for (uint32_t j = 0; j < IT; ++j) be[j] = i0 + j < k + tile ? bend[i0 + j] : 0u;
-            uint64_t tot = 0;
+            Xd mine = xd_identity();
 #pragma unroll
             for (uint32_t j = 0; j < IT; ++j) {
                 const uint32_t b = i0 + j;
-                inc[j] = 0;
-                if (b < k + tile) {
-                    const uint32_t cnt = be[j] - prev;
-                    prev = be[j];
-                    if (cnt) {
-                        nem |= 1u << j;
-                        const Term t = term_of(bits_f32(bucket_top(b) - 1u), bd.E);
-                        if (((XL.topv[b >> 5] >> (b & 31u)) & 1u) || t.c0 != t.c1) evm |= 1u << j;
-                        else inc[j] = (uint64_t)cnt * t.c0;
+                bx[j] = xd_identity();
+                if (b >= k + tile) continue;
+                const uint32_t bs = prev, cnt = be[j] - prev;
+                prev = be[j];
+                if (!cnt) continue;
+                nem |= 1u << j;
+                const Term t = term_of(bits_f32(bucket_top(b) - 1u), bd.E);
+                uint32_t z = 0;
+                if ((XL.topv[b >> 5] >> (b & 31u)) & 1u) {
+                    if (cnt > 256u) {
+                        evm |= 1u << j;
+                        continue;
                     }
-                    tot += inc[j];
+                    for (uint32_t q = bs; q < bs + cnt; ++q) z += (uint32_t)(ck2[q] >> 32) == bucket_top(b) ? 1u : 0u;
                 }
+                if (t.c0 != t.c1) {  // not reached: the rest of a tail bucket has no tie
+                    evm |= 1u << j;
+                    continue;
+                }
+                const uint64_t ri = (uint64_t)(cnt - z) * t.c0;
+                Xd rest;
+                rest.inc0 = rest.inc1 = ri;
+                rest.par0 = (uint32_t)(ri & 1u);
+                rest.par1 = (uint32_t)((ri + 1u) & 1u);
+                Xd top = xd_identity(), base = xd_of(term_of(bits_f32(bucket_top(b)), bd.E));
+                for (uint32_t e = z; e; e >>= 1) {
+                    if (e & 1u) top = xd_compose(top, base);
+                    base = xd_compose(base, base);
+                }
+                bx[j] = xd_compose(top, rest);
+                mine = xd_compose(mine, bx[j]);
             }
-            // every term adds the same for either parity: a plain sum scan
-            Xd mine = xd_identity();
-            mine.inc0 = mine.inc1 = tot;
-            mine.par0 = (uint32_t)(tot & 1u);
-            mine.par1 = (uint32_t)((tot + 1u) & 1u);
             const Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
-            uint64_t acc = (uint64_t)bd.A + pre.inc0;
+            const uint32_t b0 = bd.A & 1u;
+            uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
+            uint32_t par = b0 ? pre.par1 : pre.par0;
             uint32_t mystop = NONE;
             float stopv = 0.0f, last = 0.0f;
 #pragma unroll
             for (uint32_t j = 0; j < IT; ++j) {
                 const uint32_t b = i0 + j;
                 if (b >= k + tile || mystop != NONE) continue;
-                if (((evm >> j) & 1u) || acc + inc[j] >= (1ull << 24)) {
+                const uint64_t inc = par ? bx[j].inc1 : bx[j].inc0;
+                if (((evm >> j) & 1u) || acc + inc >= (1ull << 24)) {
                     mystop = b;
                     stopv = binade_value((uint32_t)acc, bd.E);
                     continue;
                 }
-                acc += inc[j];
+                par = par ? bx[j].par1 : bx[j].par0;
+                acc += inc;
                 last = binade_value((uint32_t)acc, bd.E);
                 if ((nem >> j) & 1u) S[be[j] - 1u] = last;
             }
@@ -3215,28 +3226,20 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             lds_barrier();
             const uint32_t kc = s_cross;
             if (kc == NONE) {
-                if (k + tile - 1u - i0 < IT) {  // this thread holds the tile's last bucket
-                    s_s = last;
-                    s_k = k + tile;
-                }
+                if (k + tile - 1u - i0 < IT) s_s = last;  // this thread holds the tile's last bucket
             } else if (mystop == kc) {
                 s_s = stopv;
-                s_k = kc;
             }
             lds_barrier();
-            if (kc != NONE) {
-                const float sb = s_s;
-                __syncthreads();  // s_s read by every thread before the bucket's sums reset it
-                const float se = bucket_elems(kc, sb);
-                if (tid == 0) {
-                    s_s = se;
-                    s_k = kc + 1u;
-                    s_cross = NONE;
-                }
-                __syncthreads();
-            } else if (tid == 0) {
-                s_cross = NONE;  // read by every thread before the barrier above
+            s = s_s;
+            if (kc == NONE) {
+                k += tile;
+                continue;
             }
+            __syncthreads();  // s_s and s_cross read by every thread
+            if (tid == 0) s_cross = NONE;
+            s = bucket_elems(kc, s);  // resets s_cross itself
+            k = kc + 1u;
         }
         __threadfence_block();
         __syncthreads();
