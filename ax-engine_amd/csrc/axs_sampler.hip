@@ -1824,6 +1824,8 @@ constexpr uint32_t RERR_CAP = 4u;          // more than CAPP captures
 
 // LDS of the exact path's sort and running sums (one row per workgroup)
 constexpr uint32_t NMIXW = NBUCKET / 32;
+constexpr uint32_t NTAILB = 5120;                  // tail buckets: p in [2^-24, 2^-14)
+constexpr uint32_t BEND_STRIDE = NBUCKET + NTAILB;  // per row: bucket ends, top-value counts
 struct ExLds {
     uint32_t cnt[NBUCKET];  // bucket counts, then bucket ends; then sort scratch
     uint64_t stage[(NT_EX / 64) * 128];  // each wave's window of keys
@@ -1833,7 +1835,7 @@ struct ExLds {
     Xd w[NT_EX / 64];
     uint32_t u[NT_EX / 64];
     float s;
-    uint32_t k, cross, err;
+    uint32_t k, cross, err, xc;
 };
 
 struct RowLds {
@@ -2628,6 +2630,9 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     // sorted laws keep only p >= pmin: below ln(min(pmin, min_p)) - 0.7 the
     // exp is under half of both (no key, and no min-p boundary), so it is skipped
     const double xskip = xsorted ? log((double)(xminp ? fminf(xs.pmin, c.p.min_p) : xs.pmin)) - 0.7 : -INFINITY;
+    // each wave's staging slots for the elements whose exp is computed
+    static_assert(sizeof(ExLds) >= (size_t)RWV * 64u * EPV * sizeof(uint64_t), "staging slots");
+    uint64_t* xstg = reinterpret_cast<uint64_t*>(&SL.ex) + (size_t)(tid >> 6) * 64u * EPV;
     const bool hok = !(SL.err & RERR_HASH);
     float* dense = a.dense + (size_t)r * a.vocab;
     uint64_t* ck = a.ckey + (size_t)r * a.vocab;
@@ -2662,39 +2667,86 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             const uint32_t sk = e0 < hi ? spec_bits(e0) : 0u;
             float v[EPV];
             vec_vals(T.raw[j], mw, e0, sk, v);
-            uint32_t km = 0;
-#pragma unroll
-            for (int q = 0; q < EPV; ++q) {
-                const uint32_t e = e0 + (uint32_t)q;
-                if ((sk >> q) & 1u) v[q] = xval(e, unpack<DT>(T.raw[j], q), MASK && !((mw >> (e & 31u)) & 1u));
-                const float pr = prob_of_above(v[q], xs.m, xs.inv, xskip);
-                bool keep = true;
-                if (xminp) {
-                    if (!isnan(v[q]) && e < hi && pr > 0.0f) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
-                    keep = pr >= c.p.min_p;
-                }
-                v[q] = keep ? pr : 0.0f;
-                if (e < hi) {
-                    if (!xsorted) dense[e] = v[q];
-                    else if (v[q] >= xs.pmin) km |= 1u << q;
-                }
-            }
             if (xsorted) {
-                // the wave's keys, at one LDS claim per vector
-                const uint32_t mine = (uint32_t)__popc(km);
-                uint32_t incl = mine;
+                // x = (l - m) * inv of each element; those at or above the
+                // skip bound are staged (x, id) in the wave's LDS slots, so
+                // that the exp runs on full waves
+                uint32_t cm = 0;
+                float xq[EPV];
+#pragma unroll
+                for (int q = 0; q < EPV; ++q) {
+                    const uint32_t e = e0 + (uint32_t)q;
+                    if ((sk >> q) & 1u) v[q] = xval(e, unpack<DT>(T.raw[j], q), MASK && !((mw >> (e & 31u)) & 1u));
+                    xq[q] = __fmul_rn(__fsub_rn(v[q], xs.m), xs.inv);
+                    if (e < hi && (double)xq[q] >= xskip) cm |= 1u << q;
+                }
+                const uint32_t nc = (uint32_t)__popc(cm);
+                uint32_t incl = nc;
 #pragma unroll
                 for (int d = 1; d < 64; d <<= 1) {
                     const uint32_t y = (uint32_t)__shfl_up((int)incl, d, 64);
                     if (lane >= d) incl += y;
                 }
                 const uint32_t tot = (uint32_t)__shfl((int)incl, 63, 64);
-                uint32_t base = 0;
-                if (lane == 0 && tot) base = atomicAdd(&SL.xn, tot);
-                uint32_t o = (uint32_t)__shfl((int)base, 0, 64) + incl - mine;
+                uint32_t so = incl - nc;
 #pragma unroll
                 for (int q = 0; q < EPV; ++q)
-                    if ((km >> q) & 1u) ck[o++] = key_pdesc(v[q], e0 + (uint32_t)q);
+                    if ((cm >> q) & 1u) xstg[so++] = ((uint64_t)__float_as_uint(xq[q]) << 32) | (e0 + (uint32_t)q);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                uint64_t kk[EPV];
+                uint32_t km = 0;
+#pragma unroll
+                for (int i = 0; i < EPV; ++i) {
+                    const uint32_t t = (uint32_t)lane + 64u * (uint32_t)i;
+                    kk[i] = 0;
+                    if (64u * (uint32_t)i >= tot) continue;  // wave-uniform
+                    if (t < tot) {
+                        const uint64_t w = xstg[t];
+                        float pr = exp_ref(__uint_as_float((uint32_t)(w >> 32)));
+                        if (!isfinite(pr)) pr = 0.0f;
+                        if (xminp) {
+                            if (pr > 0.0f) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
+                            if (!(pr >= c.p.min_p)) pr = 0.0f;
+                        }
+                        if (pr >= xs.pmin) {
+                            kk[i] = key_pdesc(pr, (uint32_t)w);
+                            km |= 1u << i;
+                        }
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                // the wave's keys, at one LDS claim per vector
+                const uint32_t mine = (uint32_t)__popc(km);
+                uint32_t kin = mine;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const uint32_t y = (uint32_t)__shfl_up((int)kin, d, 64);
+                    if (lane >= d) kin += y;
+                }
+                const uint32_t ktot = (uint32_t)__shfl((int)kin, 63, 64);
+                uint32_t base = 0;
+                if (lane == 0 && ktot) base = atomicAdd(&SL.xn, ktot);
+                uint32_t o = (uint32_t)__shfl((int)base, 0, 64) + kin - mine;
+#pragma unroll
+                for (int i = 0; i < EPV; ++i)
+                    if ((km >> i) & 1u) ck[o++] = kk[i];
+                continue;
+            }
+#pragma unroll
+            for (int q = 0; q < EPV; ++q) {
+                const uint32_t e = e0 + (uint32_t)q;
+                if ((sk >> q) & 1u) v[q] = xval(e, unpack<DT>(T.raw[j], q), MASK && !((mw >> (e & 31u)) & 1u));
+                const float pr = prob_of(v[q], xs.m, xs.inv);
+                bool keep = true;
+                if (xminp) {
+                    if (!isnan(v[q]) && e < hi) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
+                    keep = pr >= c.p.min_p;
+                }
+                if (e < hi) dense[e] = keep ? pr : 0.0f;
             }
         }
     }
@@ -2906,11 +2958,12 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     const uint64_t* src = a.ckey + (size_t)r * V;
     uint64_t* keys = a.ckey2 + (size_t)r * V;
     uint64_t* sorted_keys = a.ckey + (size_t)r * V;  // written once src is consumed
-    uint32_t* bend = a.bend + (size_t)r * NBUCKET;
+    uint32_t* bend = a.bend + (size_t)r * BEND_STRIDE;
+    uint32_t* zc = bend + NBUCKET;  // copies of each tail bucket's top value
     const float* dense = a.dense + (size_t)r * V;
     float* S = a.sbuf + (size_t)r * V;
     if (tid == 0) s_err = 0;
-    uint64_t* const ck2 = keys;  // bucket-grouped keys; unsorted tail buckets stay here
+    uint64_t* const ck2 = keys;  // the head grouped by bucket, then the tail keys in any order
     // block sort of kp[st, en) by (p desc, id asc): in LDS (s_cnt) up to
     // BIG_LDS_SORT keys, else in the row's HBM scratch.  Uniform control flow.
     auto sort_range_in = [&](uint64_t* kp, uint32_t st, uint32_t en) {
@@ -2999,7 +3052,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     };
 
     // positions [0, n_head) are sorted in keys and summed element by element;
-    // the tail buckets' keys stay grouped in ck2 unless tail_all
+    // the tail keys stay unordered in ck2[n_head, n) unless tail_all
     uint32_t n_head = n;
     bool tail_all = true;
     if (sorted) {
@@ -3010,6 +3063,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             XL.topv[i] = 0;
             XL.done[i] = 0;
         }
+        if (tid == 0) s_k = 0;
         __syncthreads();
         constexpr uint32_t U = XI;  // keys per thread per round, every load issued first
         for (uint32_t i0 = tid; i0 < n; i0 += NT_EX * U) {
@@ -3021,8 +3075,13 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
                 if (i0 + u * NT_EX < n) {
                     const uint32_t b = bucket_of(kk[u]);
                     atomicAdd(&s_cnt[b], 1u);
-                    if (b >= NHB && (uint32_t)(kk[u] >> 32) == bucket_top(b))
+                    if (b >= NHB && (uint32_t)(kk[u] >> 32) == bucket_top(b)) {
                         atomicOr(&XL.topv[b >> 5], 1u << (b & 31u));
+                        // zero before the call; waited for here, so that the
+                        // count is complete before any later read
+                        const uint32_t old = atomicAdd(&zc[b - NHB], 1u);
+                        asm volatile("" ::"v"(old));
+                    }
                 }
         }
         __syncthreads();
@@ -3037,20 +3096,36 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             pre += c;
         }
         __syncthreads();
+        // head keys to their bucket's range; tail keys appended after the
+        // head in any order (one claim per wave and round)
+        n_head = s_cnt[NHB];
+        const int lane = tid & 63;
         for (uint32_t i0 = tid; i0 < n; i0 += NT_EX * U) {
             uint64_t kk[U];
 #pragma unroll
             for (uint32_t u = 0; u < U; ++u) kk[u] = i0 + u * NT_EX < n ? src[i0 + u * NT_EX] : 0ull;
 #pragma unroll
-            for (uint32_t u = 0; u < U; ++u)
-                if (i0 + u * NT_EX < n) keys[atomicAdd(&s_cnt[bucket_of(kk[u])], 1u)] = kk[u];
+            for (uint32_t u = 0; u < U; ++u) {
+                const bool ok = i0 + u * NT_EX < n;
+                const uint32_t b = bucket_of(kk[u]);
+                if (ok && b < NHB) keys[atomicAdd(&s_cnt[b], 1u)] = kk[u];
+                const uint64_t tm = __ballot(ok && b >= NHB);
+                if (tm) {
+                    uint32_t base = 0;
+                    if (lane == 0) base = atomicAdd(&s_k, (uint32_t)__popcll(tm));
+                    base = (uint32_t)__shfl((int)base, 0, 64);
+                    if (ok && b >= NHB)
+                        keys[n_head + base + (uint32_t)__popcll(tm & ((1ull << lane) - 1ull))] = kk[u];
+                }
+            }
         }
         __threadfence_block();
         __syncthreads();
-        // s_cnt[b] is now the end of bucket b; kept in HBM for the phases
-        // that reuse s_cnt as sort scratch
-        for (uint32_t i = tid; i < NBUCKET; i += NT_EX) bend[i] = s_cnt[i];
-        n_head = s_cnt[NHB - 1];
+        // s_cnt[b] is now the end of head bucket b and the start of tail
+        // bucket b; bucket ends kept in HBM for the phases that reuse s_cnt
+        // as sort scratch
+        for (uint32_t i = tid; i < NBUCKET; i += NT_EX)
+            bend[i] = i < NHB ? s_cnt[i] : (i + 1u < NBUCKET ? s_cnt[i + 1u] : n);
         tail_all = n_head >= n;
         window_sort(keys, sorted_keys, 0u, n_head);
         keys = sorted_keys;
@@ -3134,23 +3209,46 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         __syncthreads();
         return s;
     };
-    // tail bucket b sorted in ck2 and summed element by element from the sum
-    // before it (whole block, once per bucket)
+    // tail bucket b extracted to its range of keys, sorted, and summed element
+    // by element from the sum before it (whole block, once per bucket)
     auto bucket_elems = [&](uint32_t b, float sb) -> float {
         const uint32_t bs = bend[b - 1], be = bend[b];
-        sort_range_in(ck2, bs, be);
-        const float se = elem_sums(ck2, bs, be, sb);
+        if (!tail_all) {
+            // the bucket's keys, from the unordered tail, to its range of keys
+            if (tid == 0) XL.xc = 0;
+            __syncthreads();
+            const int lane = tid & 63;
+            for (uint32_t i0 = n_head + (uint32_t)tid; i0 < n; i0 += NT_EX * IT) {
+                uint64_t kk[IT];
+#pragma unroll
+                for (uint32_t u = 0; u < IT; ++u) kk[u] = i0 + u * NT_EX < n ? ck2[i0 + u * NT_EX] : 0ull;
+#pragma unroll
+                for (uint32_t u = 0; u < IT; ++u) {
+                    const bool hit = i0 + u * NT_EX < n && bucket_of(kk[u]) == b;
+                    const uint64_t hm = __ballot(hit);
+                    if (hm) {
+                        uint32_t base = 0;
+                        if (lane == 0) base = atomicAdd(&XL.xc, (uint32_t)__popcll(hm));
+                        base = (uint32_t)__shfl((int)base, 0, 64);
+                        if (hit) keys[bs + base + (uint32_t)__popcll(hm & ((1ull << lane) - 1ull))] = kk[u];
+                    }
+                }
+            }
+            __threadfence_block();
+            __syncthreads();
+        }
+        sort_range_in(keys, bs, be);
+        const float se = elem_sums(keys, bs, be, sb);
         if (tid == 0) XL.done[b >> 5] |= 1u << (b & 31u);
         __syncthreads();
         return se;
     };
     // The tail buckets [NHB, TB_END) from the sum s0 (>= 1): a round takes IT
-    // buckets per thread as terms: the copies of the top value first (their
-    // count read from the bucket's keys; a possible tie makes that term
-    // parity-dependent), then count x units for the rest.  The first bucket
-    // that would leave the binade (or a large bucket holding its top value)
-    // is sorted and summed element by element, and the next round starts
-    // after it.  S is written at each bucket's last position.
+    // buckets per thread as terms: the copies of the top value first (counted
+    // with the buckets; a possible tie makes that term parity-dependent),
+    // then count x units for the rest.  The first bucket that would leave the
+    // binade is sorted and summed element by element, and the next round
+    // starts after it.  S is written at each bucket's last position.
     auto tail_sums = [&](float s0) {
         if (tid == 0) s_cross = NONE;
         __syncthreads();
@@ -3171,19 +3269,13 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
                 const uint32_t b = i0 + j;
                 bx[j] = xd_identity();
                 if (b >= k + tile) continue;
-                const uint32_t bs = prev, cnt = be[j] - prev;
+                const uint32_t cnt = be[j] - prev;
                 prev = be[j];
                 if (!cnt) continue;
                 nem |= 1u << j;
                 const Term t = term_of(bits_f32(bucket_top(b) - 1u), bd.E);
                 uint32_t z = 0;
-                if ((XL.topv[b >> 5] >> (b & 31u)) & 1u) {
-                    if (cnt > 256u) {
-                        evm |= 1u << j;
-                        continue;
-                    }
-                    for (uint32_t q = bs; q < bs + cnt; ++q) z += (uint32_t)(ck2[q] >> 32) == bucket_top(b) ? 1u : 0u;
-                }
+                if ((XL.topv[b >> 5] >> (b & 31u)) & 1u) z = atomicAdd(&zc[b - NHB], 0u);
                 if (t.c0 != t.c1) {  // not reached: the rest of a tail bucket has no tie
                     evm |= 1u << j;
                     continue;
@@ -3246,8 +3338,20 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     };
     // the whole tail sorted into keys after the head, as the head is
     auto tail_sort_all = [&]() {
+        // the unordered tail grouped by bucket into keys, then copied back to
+        // ck2 as the window sort's source
+        for (uint32_t i = tid; i < NBUCKET; i += NT_EX) s_cnt[i] = i ? bend[i - 1u] : 0u;
+        __syncthreads();
+        for (uint32_t i = n_head + (uint32_t)tid; i < n; i += NT_EX) {
+            const uint64_t key = ck2[i];
+            keys[atomicAdd(&s_cnt[bucket_of(key)], 1u)] = key;
+        }
+        __threadfence_block();
+        __syncthreads();
+        for (uint32_t i = n_head + (uint32_t)tid; i < n; i += NT_EX) ck2[i] = keys[i];
         for (uint32_t i = tid; i < NBUCKET; i += NT_EX) s_cnt[i] = bend[i];
         for (uint32_t i = tid; i < NMIXW; i += NT_EX) XL.mixed[i] = 0;
+        __threadfence_block();
         __syncthreads();
         window_sort(ck2, keys, n_head, n);
         mixed_sorts();
@@ -3256,6 +3360,18 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     if (!sorted) {
         elem_sums(nullptr, 0u, V, 0.0f);
     } else if (n > 0) {
+        // the top-value counts, left at zero for the next call once read
+        auto reset_zc = [&]() {
+            for (uint32_t wi = tid; wi < NMIXW; wi += NT_EX) {
+                uint32_t bits = XL.topv[wi];
+                while (bits) {
+                    const uint32_t b = wi * 32u + (uint32_t)__ffs((int)bits) - 1u;
+                    bits &= bits - 1u;
+                    const uint32_t old = atomicExch(&zc[b - NHB], 0u);
+                    asm volatile("" ::"v"(old));
+                }
+            }
+        };
         const float sh = elem_sums(keys, 0u, n_head, 0.0f);
         if (!tail_all) {
             if (sh >= 1.0f) {
@@ -3266,6 +3382,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
                 n_head = n;
             }
         }
+        reset_zc();
     }
     __threadfence_block();
     __syncthreads();  // every S store complete before the decisions read S
@@ -3394,9 +3511,8 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         return S[i];
     };
     auto key_at = [&](uint32_t i) -> uint64_t {
-        if (i < n_head || tail_all) return keys[i];
-        ensure_bucket(tail_bucket_at(i));
-        return ck2[i];
+        if (i >= n_head && !tail_all) ensure_bucket(tail_bucket_at(i));
+        return keys[i];
     };
     // first position in [0, lim) with S >= t, lim if none
     auto locate = [&](float t, uint32_t lim) -> uint32_t {
@@ -3450,7 +3566,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         const uint32_t po = (a.out_kept && a.out_kept_cap > 0) ? min(Lk, (uint32_t)a.out_kept_cap) : 0u;
         const uint32_t pw = a.ws_kept_id ? min(Lk, KEPT_CAP) : 0u;
         const uint32_t P = max(po, pw);
-        const uint64_t kj0 = key_at(j);  // a tail bucket read here is sorted in ck2
+        const uint64_t kj0 = key_at(j);  // a tail bucket read here is extracted and sorted
         if (P > n_head && !tail_all) tail_sort_all();
         auto order_ids = [&](uint32_t pos) -> uint32_t {  // returns the end of pos's bucket
             const uint32_t b = bucket_of(keys[pos]);
@@ -4249,7 +4365,7 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
         (rc = dalloc(&c->row_done, R + 1)) ||
         (rc = dalloc(&c->dense, R * Vv)) || (rc = dalloc(&c->ckey, R * Vv)) ||
         (rc = dalloc(&c->ckey2, R * Vv)) || (rc = dalloc(&c->tmp64, R * (size_t)c->tmp_stride)) ||
-        (rc = dalloc(&c->sbuf, R * Vv)) || (rc = dalloc(&c->bend, R * NBUCKET)) ||
+        (rc = dalloc(&c->sbuf, R * Vv)) || (rc = dalloc(&c->bend, R * BEND_STRIDE)) ||
         (rc = dalloc(&c->kept_id, R * KEPT_CAP)) || (rc = dalloc(&c->kept_p, R * KEPT_CAP)) ||
         (rc = dalloc(&c->mtp_tok, R)) || (rc = dalloc(&c->mtp_amax, R)) || (rc = dalloc(&c->mtp_lnq, R)) ||
         (rc = dalloc(&c->lp_tok, R)) || (rc = dalloc(&c->lp_temps, R))) {
@@ -4265,6 +4381,7 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
     // the counters start at zero; every call leaves them at zero again
     if (hipMemset(c->row_done, 0, (R + 1) * sizeof(uint32_t)) != hipSuccess ||
         hipMemset(c->exact_count, 0, sizeof(uint32_t)) != hipSuccess ||
+        hipMemset(c->bend, 0, R * BEND_STRIDE * sizeof(uint32_t)) != hipSuccess ||
         hipDeviceSynchronize() != hipSuccess) {
         free_ctx(c);
         return fail(AXS_E_HIP, "clearing the workspace counters failed");
