@@ -105,16 +105,6 @@ __device__ __forceinline__ float prob_of(float l, float m, float inv) {
     return isfinite(p) ? p : 0.0f;
 }
 
-// prob_of for a row whose small probabilities are not needed: 0 without
-// the exp when x = (l - m) * inv is below `skip` (a double bound chosen so
-// that exp(x) is known to be below the row's floor there)
-__device__ __forceinline__ float prob_of_above(float l, float m, float inv, double skip) {
-    const float x = __fmul_rn(__fsub_rn(l, m), inv);
-    if ((double)x < skip) return 0.0f;
-    const float p = exp_ref(x);
-    return isfinite(p) ? p : 0.0f;
-}
-
 // ln x rounded once to f32 (glibc's logf, which the reference calls, is
 // correctly rounded for nearly all inputs)
 __device__ __forceinline__ float ln_f32(float x) { return (float)log((double)x); }

@@ -1836,6 +1836,8 @@ struct ExLds {
     uint32_t u[NT_EX / 64];
     float s;
     uint32_t k, cross, err, xc;
+    uint32_t npc;             // predicted crossings of the tile
+    uint32_t pc[32];          // ... their positions
 };
 
 struct RowLds {
@@ -1894,6 +1896,24 @@ __device__ __forceinline__ float minp_edge(float min_p) {
         else lo = mid;
     }
     return ord2f(hi);
+}
+
+// Bounds of a sorted row's exact path, on x = (l - m) * inv: the keys are the
+// elements with x >= xe (p >= pmin: exp_ref is monotone), and the min-p
+// boundary flag reads the elements with x in [xm0, xm1) (p within 2e-6
+// relative of min_p; the flag's 1e-6 margin lies inside).
+struct KeyEdge {
+    float xe, xm0, xm1;
+};
+__device__ __forceinline__ KeyEdge key_edges(float pmin, bool minp, float min_p) {
+    KeyEdge k;
+    k.xe = minp_edge(pmin);
+    k.xm0 = k.xm1 = INFINITY;
+    if (minp) {
+        k.xm0 = minp_edge(min_p * (1.0f - 2e-6f));
+        k.xm1 = minp_edge(min_p * (1.0f + 2e-6f));
+    }
+    return k;
 }
 
 // home slot of id t: the murmur3 finalizer, so that arithmetic progressions
@@ -2627,9 +2647,9 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     }
     const bool xminp = xs.mode == M_MINP;
     const bool xsorted = xs.sorted != 0;
-    // sorted laws keep only p >= pmin: below ln(min(pmin, min_p)) - 0.7 the
-    // exp is under half of both (no key, and no min-p boundary), so it is skipped
-    const double xskip = xsorted ? log((double)(xminp ? fminf(xs.pmin, c.p.min_p) : xs.pmin)) - 0.7 : -INFINITY;
+    // sorted laws: the exp only for keys and near the min-p boundary
+    const KeyEdge ke = key_edges(xs.pmin, xminp, c.p.min_p);
+    const float xstage = fminf(ke.xe, ke.xm0);
     // each wave's staging slots for the elements whose exp is computed
     static_assert(sizeof(ExLds) >= (size_t)RWV * 64u * EPV * sizeof(uint64_t), "staging slots");
     uint64_t* xstg = reinterpret_cast<uint64_t*>(&SL.ex) + (size_t)(tid >> 6) * 64u * EPV;
@@ -2668,9 +2688,9 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
             float v[EPV];
             vec_vals(T.raw[j], mw, e0, sk, v);
             if (xsorted) {
-                // x = (l - m) * inv of each element; those at or above the
-                // skip bound are staged (x, id) in the wave's LDS slots, so
-                // that the exp runs on full waves
+                // x = (l - m) * inv of each element; the keys (x >= xe) and
+                // those near the min-p boundary are staged (x, id) in the
+                // wave's LDS slots, so that the exp runs on full waves
                 uint32_t cm = 0;
                 float xq[EPV];
 #pragma unroll
@@ -2678,7 +2698,7 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                     const uint32_t e = e0 + (uint32_t)q;
                     if ((sk >> q) & 1u) v[q] = xval(e, unpack<DT>(T.raw[j], q), MASK && !((mw >> (e & 31u)) & 1u));
                     xq[q] = __fmul_rn(__fsub_rn(v[q], xs.m), xs.inv);
-                    if (e < hi && (double)xq[q] >= xskip) cm |= 1u << q;
+                    if (e < hi && xq[q] >= xstage) cm |= 1u << q;
                 }
                 const uint32_t nc = (uint32_t)__popc(cm);
                 uint32_t incl = nc;
@@ -2704,13 +2724,11 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                     if (64u * (uint32_t)i >= tot) continue;  // wave-uniform
                     if (t < tot) {
                         const uint64_t w = xstg[t];
-                        float pr = exp_ref(__uint_as_float((uint32_t)(w >> 32)));
+                        const float x = __uint_as_float((uint32_t)(w >> 32));
+                        float pr = exp_ref(x);
                         if (!isfinite(pr)) pr = 0.0f;
-                        if (xminp) {
-                            if (pr > 0.0f) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
-                            if (!(pr >= c.p.min_p)) pr = 0.0f;
-                        }
-                        if (pr >= xs.pmin) {
+                        if (x >= ke.xm0 && x < ke.xm1) xmg = fminf(xmg, fabsf(pr - c.p.min_p) / c.p.min_p);
+                        if (x >= ke.xe) {
                             kk[i] = key_pdesc(pr, (uint32_t)w);
                             km |= 1u << i;
                         }
@@ -2774,7 +2792,9 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
     __shared__ ProcLds<NT_CHUNK, EX_SEGMAX> L;
     __shared__ uint32_t s_u[NT_CHUNK / 64];
     __shared__ float s_f[NT_CHUNK / 64];
-    __shared__ uint32_t s_base;
+    __shared__ uint32_t s_base, s_cur;
+    constexpr int EPVC = Ev<DT>::EPV;
+    __shared__ uint64_t s_stg[(NT_CHUNK / 64) * 64 * EPVC];  // each wave's staged (x, id)
     const int tid = threadIdx.x;
     const uint32_t nex = *a.exact_count;
     const int64_t total = (int64_t)nex * a.nch;
@@ -2799,42 +2819,102 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
         float mg = INFINITY;
         uint32_t cnt = 0;
         float* dense = a.dense + (size_t)r * a.vocab;
-        // sorted laws keep only p >= pmin: below ln(min(pmin, min_p)) - 0.7 the
-        // exp is under half of both (no key, and no min-p boundary), so it is skipped
-        const double skip = rs.sorted ? log((double)(minp ? fminf(rs.pmin, minp_v) : rs.pmin)) - 0.7 : -INFINITY;
-        // pass 1: exact probabilities; dense rows are written here, sorted rows
-        // only counted
-        auto pass1 = [&](uint32_t e, float l) {
-            float pr = prob_of_above(l, rs.m, rs.inv, skip);
-            bool keep = true;
-            if (minp) {
-                if (!isnan(l) && pr > 0.0f) mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
-                keep = pr >= minp_v;
-            }
-            float v = keep ? pr : 0.0f;
-            if (!rs.sorted) {
-                if (e < hi) dense[e] = v;
-            } else if (v >= rs.pmin) {
-                ++cnt;
-            }
-        };
-        regs_visit<DT, NV>(c, L, lo, S, special, pass1);
-        if (special) visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass1);
-        if (rs.sorted) {
-            uint32_t tot;
-            uint32_t pre = block_excl_scan_u32<NT_CHUNK>(cnt, s_u, &tot);
-            if (tid == 0) s_base = tot ? atomicAdd(&a.rstate[r].ncompact, tot) : 0u;
-            __syncthreads();
-            uint64_t* dst = a.ckey + (size_t)r * a.vocab + s_base + pre;
-            uint32_t o = 0;
-            // pass 2: write the compacted (p desc, id asc) keys
-            auto pass2 = [&](uint32_t e, float l) {
-                float pr = prob_of_above(l, rs.m, rs.inv, skip);
-                if (minp && !(pr >= minp_v)) pr = 0.0f;
-                if (pr >= rs.pmin) dst[o++] = key_pdesc(pr, e);
+        if (!rs.sorted) {
+            // index-order rows: every probability, written to the dense row
+            auto pass_dense = [&](uint32_t e, float l) {
+                const float pr = prob_of(l, rs.m, rs.inv);
+                bool keep = true;
+                if (minp) {
+                    if (!isnan(l)) mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
+                    keep = pr >= minp_v;
+                }
+                if (e < hi) dense[e] = keep ? pr : 0.0f;
             };
-            regs_visit<DT, NV>(c, L, lo, S, special, pass2);
-            if (special) visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass2);
+            regs_visit<DT, NV>(c, L, lo, S, special, pass_dense);
+            if (special) visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass_dense);
+        } else {
+            // sorted rows: the keys are the elements with x >= xe; counted
+            // first (no exp), then written with the exp run on full waves
+            const KeyEdge ke = key_edges(rs.pmin, minp, minp_v);
+            auto xof = [&](float l) { return __fmul_rn(__fsub_rn(l, rs.m), rs.inv); };
+            auto margin = [&](float x) {
+                if (x >= ke.xm0 && x < ke.xm1) {
+                    float pr = exp_ref(x);
+                    if (!isfinite(pr)) pr = 0.0f;
+                    mg = fminf(mg, fabsf(pr - minp_v) / minp_v);
+                }
+            };
+            auto pass1 = [&](uint32_t e, float l) {
+                const float x = xof(l);
+                if (e < hi && x >= ke.xe) ++cnt;
+                if (minp && e < hi) margin(x);
+            };
+            regs_visit<DT, NV>(c, L, lo, S, special, pass1);
+            if (special) visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass1);
+            uint32_t tot;
+            block_excl_scan_u32<NT_CHUNK>(cnt, s_u, &tot);
+            if (tid == 0) {
+                s_base = tot ? atomicAdd(&a.rstate[r].ncompact, tot) : 0u;
+                s_cur = 0;
+            }
+            __syncthreads();
+            uint64_t* dst = a.ckey + (size_t)r * a.vocab + s_base;
+            const int lane = tid & 63;
+            uint64_t* stg = s_stg + (size_t)(tid >> 6) * 64u * EPVC;
+            // pass 2, the elements held in registers: per vector, the wave's
+            // keys staged (x, id), their exp, one LDS claim per wave
+#pragma unroll
+            for (int j = 0; j < NV; ++j) {
+                asm volatile("" : "+v"(S.raw[j]));
+                const uint32_t e0 = lo + ((uint32_t)j * NT_CHUNK + tid) * EPVC;
+                const uint32_t off0 = e0 - lo;
+                uint32_t sk = 0;
+                if (special) sk = (L.spec[off0 >> 5] >> (off0 & 31u)) & ((1u << EPVC) - 1u);
+                uint32_t cm = 0;
+                float xq[EPVC];
+#pragma unroll
+                for (int q = 0; q < EPVC; ++q) {
+                    float l = unpack<DT>(S.raw[j], q);
+                    if (c.mask_on && !((S.mw[j] >> ((e0 + q) & 31u)) & 1u)) l = -INFINITY;
+                    xq[q] = xof(l);
+                    if (!((sk >> q) & 1u) && e0 + q < hi && xq[q] >= ke.xe) cm |= 1u << q;
+                }
+                const uint32_t nc = (uint32_t)__popc(cm);
+                uint32_t incl = nc;
+#pragma unroll
+                for (int d = 1; d < 64; d <<= 1) {
+                    const uint32_t y = (uint32_t)__shfl_up((int)incl, d, 64);
+                    if (lane >= d) incl += y;
+                }
+                const uint32_t wt = (uint32_t)__shfl((int)incl, 63, 64);
+                if (!wt) continue;  // wave-uniform
+                uint32_t so = incl - nc;
+#pragma unroll
+                for (int q = 0; q < EPVC; ++q)
+                    if ((cm >> q) & 1u) stg[so++] = ((uint64_t)__float_as_uint(xq[q]) << 32) | (e0 + (uint32_t)q);
+                uint32_t base = 0;
+                if (lane == 0) base = atomicAdd(&s_cur, wt);
+                base = (uint32_t)__shfl((int)base, 0, 64);
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                for (uint32_t t = (uint32_t)lane; t < wt; t += 64u) {
+                    const uint64_t w = stg[t];
+                    const float pr = exp_ref(__uint_as_float((uint32_t)(w >> 32)));
+                    dst[base + t] = key_pdesc(pr, (uint32_t)w);
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            // the special elements (their processed values), one claim each
+            if (special) {
+                auto pass2s = [&](uint32_t e, float l) {
+                    const float x = xof(l);
+                    if (e < hi && x >= ke.xe) dst[atomicAdd(&s_cur, 1u)] = key_pdesc(exp_ref(x), e);
+                };
+                visit_specials<DT, NT_CHUNK, EX_SEGMAX>(a, c, L, ranked, 0u, r, rp, lo, hi, pass2s);
+            }
         }
         if (minp) {
             mg = block_max<NT_CHUNK>(-mg, s_f);
@@ -3139,9 +3219,14 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     // A tile of IT terms per thread is loaded once; a scan adds the terms in
     // the binade of the current sum, and the first term that would leave it
     // (the earliest crossing over the block) is added directly by its
-    // thread; the rest of the tile is scanned again in the new binade.  The
-    // barriers are LDS-only: S is read only after the loop.
+    // thread; the rest of the tile is scanned again in the new binade.  Each
+    // scan covers a window of the tile that ends a margin after the next
+    // position where the real-valued prefix sum (fixed point, 2^-40) passes a
+    // power of two: the rounded sum crosses there or close by, and a window
+    // without a crossing only means one more scan.  The barriers are
+    // LDS-only: S is read only after the loop.
     constexpr uint32_t IT = XI;
+    constexpr uint32_t WMARGIN = 128;
     auto elem_sums = [&](const uint64_t* kp, uint32_t k0, uint32_t kend, float s0) -> float {
         auto X = [&](uint32_t i) -> float { return kp ? pdesc_p(kp[i]) : dense[i]; };
         if (tid == 0) s_cross = NONE;
@@ -3153,15 +3238,48 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
             float xv[IT];
 #pragma unroll
             for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
+            // predicted crossings: the real prefix from the tile's start sum
+            {
+                uint64_t loc = 0;
+#pragma unroll
+                for (uint32_t j = 0; j < IT; ++j) loc += (uint64_t)((double)xv[j] * 0x1p40);
+                Xd fx = xd_identity();
+                fx.inc0 = fx.inc1 = loc;
+                const uint64_t rb = block_excl_scan_xd<NT_EX>(fx, s_w).inc0;
+                if (tid == 0) XL.npc = 0;
+                lds_barrier();
+                double rs = (double)s + (double)rb * 0x1p-40;
+                int eprev = ilogb(rs > 0.0 ? rs : 0x1p-1000);
+#pragma unroll
+                for (uint32_t j = 0; j < IT; ++j) {
+                    if (i0 + j >= k + tile) continue;
+                    rs += (double)(uint64_t)((double)xv[j] * 0x1p40) * 0x1p-40;
+                    const int e = ilogb(rs > 0.0 ? rs : 0x1p-1000);
+                    if (e > eprev) {
+                        const uint32_t slot = atomicAdd(&XL.npc, 1u);
+                        if (slot < 32u) XL.pc[slot] = i0 + j;
+                    }
+                    eprev = e;
+                }
+                lds_barrier();
+            }
+            const uint32_t npc = min(XL.npc, 32u);
             uint32_t kk = k;  // the tile's first term not yet added
             while (true) {
+                // the window [kk, we)
+                uint32_t nxt = NONE;
+                for (uint32_t q = 0; q < npc; ++q) {
+                    const uint32_t pq = XL.pc[q];
+                    if (pq >= kk && pq < nxt) nxt = pq;
+                }
+                const uint32_t we = nxt == NONE ? k + tile : min(k + tile, nxt + 1u + WMARGIN);
                 const Binade bd = binade_of(s);
                 Term t[IT];
                 Xd mine = xd_identity();
 #pragma unroll
                 for (uint32_t j = 0; j < IT; ++j) {
                     t[j].c0 = t[j].c1 = 0u;
-                    if (i0 + j >= kk && i0 + j < k + tile) {
+                    if (i0 + j >= kk && i0 + j < we) {
                         t[j] = term_of(xv[j], bd.E);
                         mine = xd_compose(mine, xd_of(t[j]));
                     }
@@ -3175,7 +3293,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
 #pragma unroll
                 for (uint32_t j = 0; j < IT; ++j) {
                     const uint32_t i = i0 + j;
-                    if (i < kk || i >= k + tile || mycross != NONE) continue;
+                    if (i < kk || i >= we || mycross != NONE) continue;
                     const uint32_t cc = par ? t[j].c1 : t[j].c0;
                     if (acc + cc >= (1ull << 24)) {
                         mycross = i;
@@ -3191,19 +3309,23 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
                 lds_barrier();
                 const uint32_t kc = s_cross;
                 if (kc == NONE) {
-                    if (k + tile - 1u - i0 < IT) s_s = last;  // this thread holds the tile's last term
+                    if (we - 1u - i0 < IT) s_s = last;  // this thread holds the window's last term
                 } else if (mycross == kc) {
                     S[kc] = xs;
                     s_s = xs;
                 }
                 lds_barrier();
                 s = s_s;  // rewritten only after the next scan's barriers
-                if (kc == NONE) break;
-                if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
-                kk = kc + 1u;
+                if (kc == NONE) {
+                    kk = we;
+                } else {
+                    if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
+                    kk = kc + 1u;
+                }
                 if (kk >= k + tile) break;
             }
             k += tile;
+            lds_barrier();  // XL.pc read by every thread before the next tile rewrites it
         }
         __threadfence_block();
         __syncthreads();
