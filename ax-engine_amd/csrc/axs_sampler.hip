@@ -3797,10 +3797,11 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
     __shared__ uint64_t s_t[KEPT_CAP];
     __shared__ uint64_t s_d[KEPT_CAP];
     __shared__ float s_v[KEPT_CAP];     // residual terms (then their normalised values) in walk order
-    __shared__ uint32_t s_id[KEPT_CAP]; // ... and their ids
+    __shared__ __align__(16) uint32_t s_id[KEPT_CAP]; // ... and their ids
     __shared__ int s_ft, s_fd;
-    __shared__ float s_rsum;
-    __shared__ uint32_t s_rn;
+    __shared__ float s_rsum, s_total;
+    __shared__ uint32_t s_cr;
+    __shared__ uint64_t s_mx;
     __shared__ uint32_t s_corr;
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
@@ -3903,18 +3904,39 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         // reference's sequential f32 sums run on one thread over LDS.
         const float ut = mtp_uniform(a, b, tp, stream ? nu : (uint32_t)D);
         const uint32_t nt = rt.nlist, nd = has_dd ? rd.nlist : 1u;
-        uint32_t npt = next_pow2(nt > 0 ? nt : 1), npd = next_pow2(nd > 0 ? nd : 1);
-        for (uint32_t k = tid; k < npt; k += NT_MTP)
-            s_t[k] = k < nt ? (((uint64_t)(~tid_l[k]) << 32) | __float_as_uint(__fdiv_rn(tp_l[k], rt.F))) : 0ull;
+        // a kept list to ascending id order: each entry's position is the
+        // number of smaller ids (the ids of a list are distinct), counted
+        // over the list staged in LDS (broadcast reads, no sorting network)
+        auto id_order = [&](const uint32_t* ids, const float* ps, float F, uint32_t n, uint64_t* dst) {
+            for (uint32_t k = tid; k < n; k += NT_MTP) {
+                s_id[k] = ids[k];
+                s_v[k] = __fdiv_rn(ps[k], F);
+            }
+            __syncthreads();
+            for (uint32_t k = tid; k < n; k += NT_MTP) {
+                const uint32_t idk = s_id[k];
+                uint32_t rk = 0, j = 0;
+                for (; j + 16u <= n; j += 16u) {  // four 16-byte reads in flight
+                    u32x4 w[4];
+#pragma unroll
+                    for (int h = 0; h < 4; ++h) w[h] = *reinterpret_cast<const u32x4*>(&s_id[j + 4u * (uint32_t)h]);
+#pragma unroll
+                    for (int h = 0; h < 4; ++h)
+                        rk += (w[h][0] < idk ? 1u : 0u) + (w[h][1] < idk ? 1u : 0u) + (w[h][2] < idk ? 1u : 0u) +
+                              (w[h][3] < idk ? 1u : 0u);
+                }
+                for (; j < n; ++j) rk += s_id[j] < idk ? 1u : 0u;
+                dst[rk] = ((uint64_t)(~idk) << 32) | __float_as_uint(s_v[k]);
+            }
+            __syncthreads();
+        };
+        id_order(tid_l, tp_l, rt.F, nt, s_t);
         if (has_dd) {
-            for (uint32_t k = tid; k < npd; k += NT_MTP)
-                s_d[k] = k < nd ? (((uint64_t)(~did_l[k]) << 32) | __float_as_uint(__fdiv_rn(dp_l[k], rd.F))) : 0ull;
-        } else if (tid == 0) {
-            s_d[0] = ((uint64_t)(~d) << 32) | __float_as_uint(1.0f);
+            id_order(did_l, dp_l, rd.F, nd, s_d);
+        } else {
+            if (tid == 0) s_d[0] = ((uint64_t)(~d) << 32) | __float_as_uint(1.0f);
+            __syncthreads();
         }
-        __syncthreads();
-        block_sort_desc<NT_MTP>(s_t, npt);  // descending ~id = ascending id
-        block_sort_desc<NT_MTP>(s_d, npd);
         for (uint32_t k = tid; k < nt; k += NT_MTP) {
             const uint32_t id = idasc_id(s_t[k]);
             uint32_t lo = 0, hi = nd;
@@ -3928,26 +3950,43 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
             s_id[k] = id;
         }
         __syncthreads();
-        if (tid == 0) {
-            float rsum = 0.0f;
-            uint32_t rn = 0;
-            for (uint32_t k = 0; k < nt; ++k) {
-                const float v = s_v[k];
-                if (v > 0.0f && isfinite(v)) {
-                    rsum = __fadd_rn(rsum, v);
-                    ++rn;
+        // The reference's sequential f32 sums: the terms prepared by every
+        // thread (a skipped term as +0, which leaves a non-negative f32 sum
+        // unchanged), the adds on one thread with LDS reads issued eight at
+        // a time (the residual's early terms leave the sum's binade almost
+        // every time, which makes a parallel exact scan slower here).  The
+        // id-ordered lists are no longer read: s_t holds the terms, s_d the
+        // running sums of the draw.
+        float* s_w = reinterpret_cast<float*>(s_t);
+        float* s_c = reinterpret_cast<float*>(s_d);
+        constexpr uint32_t RB = 8;
+        auto seq_sum = [&](bool keep) -> float {  // thread 0; running sums to s_c if keep
+            float sum = 0.0f;
+            for (uint32_t k0 = 0; k0 < nt; k0 += RB) {
+                float v[RB];
+#pragma unroll
+                for (uint32_t q = 0; q < RB; ++q) v[q] = k0 + q < nt ? s_w[k0 + q] : 0.0f;
+#pragma unroll
+                for (uint32_t q = 0; q < RB; ++q) {
+                    sum = __fadd_rn(sum, v[q]);
+                    if (keep && k0 + q < nt) s_c[k0 + q] = sum;
                 }
             }
-            s_rsum = rsum;
-            s_rn = rn;
+            return sum;
+        };
+        for (uint32_t k = tid; k < nt; k += NT_MTP) {
+            const float v = s_v[k];
+            s_w[k] = (v > 0.0f && isfinite(v)) ? v : 0.0f;
         }
         __syncthreads();
+        if (tid == 0) s_rsum = seq_sum(false);
+        __syncthreads();
         const float rsum = s_rsum;
-        if (s_rn > 0 && rsum > 0.0f && isfinite(rsum)) {
+        if (rsum > 0.0f && isfinite(rsum)) {  // some term is > 0
             // normalised residual, then sample_from_token_distribution
             for (uint32_t k = tid; k < nt; k += NT_MTP) {
-                const float v = s_v[k];
-                s_v[k] = (v > 0.0f && isfinite(v)) ? __fdiv_rn(v, rsum) : -1.0f;
+                const float w = s_w[k];
+                s_v[k] = w > 0.0f ? __fdiv_rn(w, rsum) : -1.0f;
             }
         } else {
             // empty residual: the target itself, in its kept order (sampling.rs:749)
@@ -3957,29 +3996,31 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
             }
         }
         __syncthreads();
+        for (uint32_t k = tid; k < nt; k += NT_MTP) {
+            const float q = s_v[k];
+            s_w[k] = q < 0.0f ? 0.0f : q;
+        }
         if (tid == 0) {
-            float total = 0.0f;
-            for (uint32_t k = 0; k < nt; ++k) {
-                const float q = s_v[k];
-                if (!(q < 0.0f)) total = __fadd_rn(total, q);
-            }
-            const float thr = __fmul_rn(ut, total);
-            float cum = 0.0f, bp = -1.0f;
-            uint32_t last_id = NONE, cr = NONE;
-            for (uint32_t k = 0; k < nt; ++k) {
-                const float q = s_v[k];
-                if (q < 0.0f) continue;
-                cum = __fadd_rn(cum, q);
-                if (q >= bp) {
-                    bp = q;
-                    last_id = s_id[k];
-                }
-                if (cum >= thr) {
-                    cr = s_id[k];
-                    break;
-                }
-            }
-            s_corr = cr == NONE ? last_id : cr;
+            s_cr = NONE;
+            s_mx = 0ull;
+        }
+        __syncthreads();
+        if (tid == 0) s_total = seq_sum(true);
+        __syncthreads();
+        // the draw: the first listed entry whose running sum reaches u *
+        // total; else the last of the largest entries
+        const float thr = __fmul_rn(ut, s_total);
+        for (uint32_t k = tid; k < nt; k += NT_MTP) {
+            const float q = s_v[k];
+            if (q < 0.0f) continue;
+            if (s_c[k] >= thr) atomicMin(&s_cr, k);
+            atomicMax(&s_mx, ((uint64_t)__float_as_uint(q) << 32) | (k + 1u));
+        }
+        __syncthreads();
+        if (tid == 0) {
+            const uint32_t cr = s_cr;
+            const uint64_t mx = s_mx;
+            s_corr = cr != NONE ? s_id[cr] : (mx ? s_id[(uint32_t)mx - 1u] : NONE);
         }
         __syncthreads();
         corr = s_corr;
