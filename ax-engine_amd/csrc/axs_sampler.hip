@@ -3229,6 +3229,30 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     constexpr uint32_t WMARGIN = 128;
     auto elem_sums = [&](const uint64_t* kp, uint32_t k0, uint32_t kend, float s0) -> float {
         auto X = [&](uint32_t i) -> float { return kp ? pdesc_p(kp[i]) : dense[i]; };
+        if (kend - k0 <= 256u) {
+            // a short range: the reference's own loop on one thread, its
+            // loads issued eight at a time (cheaper than the scan's barriers)
+            if (tid == 0) {
+                float s = s0;
+                for (uint32_t i0 = k0; i0 < kend; i0 += 8u) {
+                    float xv[8];
+#pragma unroll
+                    for (uint32_t j = 0; j < 8u; ++j) xv[j] = i0 + j < kend ? X(i0 + j) : 0.0f;
+#pragma unroll
+                    for (uint32_t j = 0; j < 8u; ++j)
+                        if (i0 + j < kend) {
+                            s = __fadd_rn(s, xv[j]);
+                            S[i0 + j] = s;
+                        }
+                }
+                s_s = s;
+            }
+            __threadfence_block();
+            __syncthreads();
+            const float fin = s_s;
+            __syncthreads();
+            return fin;
+        }
         if (tid == 0) s_cross = NONE;
         __syncthreads();
         float s = s0;
