@@ -3049,6 +3049,23 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     auto sort_range_in = [&](uint64_t* kp, uint32_t st, uint32_t en) {
         const uint32_t mcount = en - st;
         if (mcount <= 1) return;
+        if (mcount <= 64u) {
+            // one wave: each lane's key goes to its rank, the number of
+            // larger keys (keys are distinct: ids are)
+            if (tid < 64) {
+                const uint64_t mk = (uint32_t)tid < mcount ? kp[st + tid] : 0ull;
+                uint32_t rk = 0;
+                for (uint32_t j = 0; j < mcount; ++j) {
+                    const uint64_t kj = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(mk >> 32), (int)j, 64) << 32) |
+                                        (uint32_t)__shfl((int)(uint32_t)mk, (int)j, 64);
+                    rk += kj > mk ? 1u : 0u;
+                }
+                if ((uint32_t)tid < mcount) kp[st + rk] = mk;
+            }
+            __threadfence_block();
+            __syncthreads();
+            return;
+        }
         const uint32_t np2 = next_pow2(mcount);
         uint64_t* t = np2 <= BIG_LDS_SORT ? (uint64_t*)s_cnt : a.tmp64 + (size_t)r * a.tmp_stride;
         for (uint32_t i = tid; i < np2; i += NT_EX) t[i] = i < mcount ? kp[st + i] : 0ull;
