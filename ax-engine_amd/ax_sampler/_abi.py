@@ -69,6 +69,7 @@ EXPORTS = (
     "axs_mtp_verify",
     "axs_mtp_verify_ex",
     "axs_token_logprob_batch",
+    "axs_soft_close_probe",
     "axs_timing_enable",
     "axs_timing_read",
 )
@@ -205,6 +206,8 @@ def lib():
             L.axs_argmax_batch_noalloc.argtypes = [i32, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_token_logprob_batch.restype = i32
             L.axs_token_logprob_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
+            L.axs_soft_close_probe.restype = i32
+            L.axs_soft_close_probe.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
             L.axs_mtp_verify_ex.restype = i32
             L.axs_mtp_verify_ex.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOptions), C.POINTER(MtpOutputs), vp]
             L.axs_mtp_verify.restype = i32

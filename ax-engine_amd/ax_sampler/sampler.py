@@ -387,6 +387,25 @@ class HipSampler:
                                                   out.data_ptr(), self._stream(stream)))
         return out
 
+    def soft_close_probe(self, logits, think_ids, ranks, stream=None):
+        """think_soft_close_in_top_k per row (axs_soft_close_probe): 1 when
+        think_ids[r] is within the top ranks[r] raw logits of row r, else 0
+        (0xFFFFFFFF: declined, see the header).  Returns a device uint32 view
+        (torch int32)."""
+        torch = _torch()
+        if logits.stride(1) != 1:
+            logits = logits.contiguous()
+        B, V = logits.shape
+        tid = think_ids if isinstance(think_ids, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(np.asarray(think_ids, dtype=np.uint32)).view(np.int32)).to(self.device)
+        rk = ranks if isinstance(ranks, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(np.asarray(ranks, dtype=np.uint32)).view(np.int32)).to(self.device)
+        out = torch.empty(B, dtype=torch.int32, device=self.device)
+        _abi.check(self.L.axs_soft_close_probe(self.ctx, logits.data_ptr(), _dtype_code(logits), B, V,
+                                               logits.stride(0), tid.data_ptr(), rk.data_ptr(),
+                                               out.data_ptr(), self._stream(stream)))
+        return out
+
     def mtp_verify(self, target, draft, draft_ids, target_params, draft_params, uniforms=None,
                    stream=None, options: Optional[dict] = None) -> MtpResult:
         """target [B, D+1, V], draft [B, D, V] on device; draft_ids [B, D].

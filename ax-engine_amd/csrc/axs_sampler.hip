@@ -4094,6 +4094,127 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
     if (out_flags) out_flags[b] = flags;
 }
 
+// --------------------------------------------------------------------------
+// k_probe: think_soft_close_in_top_k per row
+// (crates/ax-engine-mlx/src/ngram_accel.rs:1609-1640)
+// --------------------------------------------------------------------------
+constexpr int NT_PROBE = 1024;
+constexpr uint32_t PROBE_RANK_CAP = 1024;  // ranks the exact replay holds
+// The reference keeps a running top set over the raw logits: the first
+// `rank` taken as they come and sorted by total order, afterwards a logit
+// replaces the last entry only when it is greater (IEEE).  Without NaN, and
+// without both signed zeros, that set is the top `rank` by (logit desc, id
+// asc): the target is in it iff fewer than `rank` logits beat it (larger, or
+// equal at a lower id) — one pass and a count.  A row with a NaN, or with
+// both -0 and +0, is replayed literally on one thread (NaNs and signed zeros
+// sort by total order but compare by IEEE).  out: 1 hit, 0 miss, NONE when a
+// replay would need more than PROBE_RANK_CAP entries.
+template <int DT>
+__global__ __launch_bounds__(NT_PROBE) void k_probe(KArgs a, const uint32_t* think_ids, const uint32_t* ranks,
+                                                      uint32_t* out_hit) {
+    __shared__ uint32_t s_beats, s_flags;
+    __shared__ uint32_t s_idx[PROBE_RANK_CAP];
+    __shared__ float s_val[PROBE_RANK_CAP];
+    const int r = blockIdx.x;
+    const int tid = threadIdx.x;
+    const uint32_t V = (uint32_t)a.vocab;
+    const uint32_t t = think_ids[r], rank = ranks[r];
+    if (rank == 0u || t >= V) {
+        if (tid == 0) out_hit[r] = 0u;
+        return;
+    }
+    const char* rp = row_ptr(a, r);
+    auto at = [&](uint32_t i) -> float {
+        if (DT == AXS_DTYPE_BF16) return __uint_as_float((uint32_t)((const uint16_t*)rp)[i] << 16);
+        return ((const float*)rp)[i];
+    };
+    if (tid == 0) {
+        s_beats = 0;
+        s_flags = 0;
+    }
+    __syncthreads();
+    const float vt = at(t);
+    uint32_t beats = 0, fl = 0;
+    constexpr uint32_t U = 8;  // loads in flight per thread
+    for (uint32_t i0 = (uint32_t)tid; i0 < V; i0 += NT_PROBE * U) {
+        float v[U];
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) v[u] = i0 + u * NT_PROBE < V ? at(i0 + u * NT_PROBE) : -INFINITY;
+#pragma unroll
+        for (uint32_t u = 0; u < U; ++u) {
+            const uint32_t i = i0 + u * NT_PROBE;
+            if (i >= V) continue;
+            beats += (v[u] > vt || (v[u] == vt && i < t)) ? 1u : 0u;
+            if (isnan(v[u])) fl |= 1u;
+            if (v[u] == 0.0f) fl |= signbit(v[u]) ? 2u : 4u;
+        }
+    }
+    beats += __shfl_xor(beats, 32, 64);
+    beats += __shfl_xor(beats, 16, 64);
+    beats += __shfl_xor(beats, 8, 64);
+    beats += __shfl_xor(beats, 4, 64);
+    beats += __shfl_xor(beats, 2, 64);
+    beats += __shfl_xor(beats, 1, 64);
+    if ((tid & 63) == 0) atomicAdd(&s_beats, beats);
+    if (fl) atomicOr(&s_flags, fl);
+    __syncthreads();
+    if (tid != 0) return;
+    const uint32_t f = s_flags;
+    if (!((f & 1u) || (f & 6u) == 6u)) {
+        out_hit[r] = s_beats < rank ? 1u : 0u;
+        return;
+    }
+    if (rank >= V) {  // every logit is in the set
+        out_hit[r] = 1u;
+        return;
+    }
+    if (rank > PROBE_RANK_CAP) {
+        out_hit[r] = NONE;
+        return;
+    }
+    // the reference's loop, literally
+    auto tkey = [](float x) -> int32_t {
+        int32_t k = __float_as_int(x);
+        return k ^ (int32_t)(((uint32_t)(k >> 31)) >> 1);
+    };
+    uint32_t len = 0;
+    for (uint32_t i = 0; i < V; ++i) {
+        const float v = at(i);
+        if (len < rank) {
+            s_idx[len] = i;
+            s_val[len] = v;
+            ++len;
+            if (len == rank)
+                for (uint32_t q = 1; q < len; ++q) {  // stable, descending total order
+                    const uint32_t ti = s_idx[q];
+                    const float tv = s_val[q];
+                    uint32_t b = q;
+                    while (b > 0 && tkey(tv) > tkey(s_val[b - 1])) {
+                        s_idx[b] = s_idx[b - 1];
+                        s_val[b] = s_val[b - 1];
+                        --b;
+                    }
+                    s_idx[b] = ti;
+                    s_val[b] = tv;
+                }
+            continue;
+        }
+        if (v > s_val[rank - 1]) {
+            uint32_t b = rank - 1;
+            while (b > 0 && tkey(v) > tkey(s_val[b - 1])) {
+                s_idx[b] = s_idx[b - 1];
+                s_val[b] = s_val[b - 1];
+                --b;
+            }
+            s_idx[b] = i;
+            s_val[b] = v;
+        }
+    }
+    uint32_t hit = 0;
+    for (uint32_t q = 0; q < len; ++q) hit |= s_idx[q] == t ? 1u : 0u;
+    out_hit[r] = hit;
+}
+
 }  // namespace axs
 
 // ==========================================================================
@@ -4871,6 +4992,34 @@ int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int
     a.out_lp = out_logprob;
     Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
     if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
+    return order_end(ctx, s);
+}
+
+int axs_soft_close_probe(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
+                         int64_t row_stride, const uint32_t* think_ids, const uint32_t* ranks,
+                         uint32_t* out_hit, void* stream) {
+    if (!ctx || !logits || !think_ids || !ranks || !out_hit)
+        return fail(AXS_E_INVALID, "ctx, logits, think_ids, ranks and out_hit must be non-NULL");
+    if (dtype != AXS_DTYPE_F32 && dtype != AXS_DTYPE_BF16) return fail(AXS_E_INVALID, "bad dtype");
+    if (batch < 1 || vocab < 1 || row_stride < vocab) return fail(AXS_E_INVALID, "bad shape");
+    if (batch > ctx->max_rows || vocab > ctx->max_vocab)
+        return fail(AXS_E_CAPACITY, "batch or vocab larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DevGuard g(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = order_begin(ctx, s);
+    if (rc) return rc;
+    KArgs a{};
+    a.logits = logits;
+    a.dtype = dtype;
+    a.nrows = batch;
+    a.vocab = vocab;
+    a.stride = row_stride;
+    if (dtype == AXS_DTYPE_BF16)
+        hipLaunchKernelGGL((k_probe<AXS_DTYPE_BF16>), dim3(batch), dim3(NT_PROBE), 0, s, a, think_ids, ranks, out_hit);
+    else
+        hipLaunchKernelGGL((k_probe<AXS_DTYPE_F32>), dim3(batch), dim3(NT_PROBE), 0, s, a, think_ids, ranks, out_hit);
+    AXS_HIP_CHECK(hipGetLastError());
     return order_end(ctx, s);
 }
 

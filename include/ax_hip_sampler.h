@@ -355,6 +355,21 @@ int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int
                             int64_t row_stride, const uint32_t* tokens, const float* temperatures,
                             float* out_logprob, void* stream);
 
+/* Think soft-close rank probe, per row: out_hit[r] = 1 when think_ids[r]
+ * sits within the top ranks[r] raw logits of row r (no processors, no
+ * temperature), else 0 — think_soft_close_in_top_k
+ * (crates/ax-engine-mlx/src/ngram_accel.rs:1609-1640), whose caller emits
+ * the think-close token on a hit and samples the row otherwise
+ * (ngram_accel.rs:1691-1713; a hit consumes no uniform).  rank 0 or an id
+ * >= vocab is a miss.  Ties go to the lower id, as the reference's running
+ * set keeps them; a row holding a NaN, or both -0 and +0, is replayed
+ * exactly as the reference's loop runs (ranks up to 1024; above that
+ * out_hit[r] = AXS_NONE_U32 and the caller runs the host probe).
+ * think_ids, ranks and out_hit are device arrays of batch entries. */
+int axs_soft_close_probe(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
+                         int64_t row_stride, const uint32_t* think_ids, const uint32_t* ranks,
+                         uint32_t* out_hit, void* stream);
+
 /* MTP speculative verify (see axs_mtp_desc). */
 /* MTP verify with options: per sequence, mtp_accept_count
  * (crates/ax-engine-mlx/src/runner/mod.rs:12333-12462) over the draft ids,

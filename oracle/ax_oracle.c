@@ -822,6 +822,62 @@ float axo_full_vocab_token_logprob(const float* logits, uint32_t n, uint32_t tok
     return fmaxf(logf(fmaxf(unnorm / sum, 1e-37f)), -30.0f);
 }
 
+/* think_soft_close_in_top_k (crates/ax-engine-mlx/src/ngram_accel.rs:1609-1640):
+ * the reference's single pass, kept literally: the first `rank` logits taken
+ * as they come and stably sorted descending by total order (f32::total_cmp);
+ * afterwards a logit replaces the last entry only when it is greater (IEEE
+ * `>`), the array re-sorted stably; membership of the target at the end. */
+static int32_t total_key(float x);
+
+int axo_soft_close_in_top_k(const float* logits, uint32_t n, uint32_t target, uint32_t rank) {
+    if (rank == 0 || n == 0) return 0;
+    if (target >= n) return 0;
+    uint32_t* idx = (uint32_t*)malloc(sizeof(uint32_t) * rank);
+    float* val = (float*)malloc(sizeof(float) * rank);
+    uint32_t len = 0;
+    for (uint32_t i = 0; i < n; ++i) {
+        float v = logits[i];
+        if (len < rank) {
+            idx[len] = i;
+            val[len] = v;
+            ++len;
+            if (len == rank) {
+                /* stable insertion sort, descending by total order */
+                for (uint32_t a = 1; a < len; ++a) {
+                    uint32_t ti = idx[a];
+                    float tv = val[a];
+                    uint32_t b = a;
+                    while (b > 0 && total_key(tv) > total_key(val[b - 1])) {
+                        idx[b] = idx[b - 1];
+                        val[b] = val[b - 1];
+                        --b;
+                    }
+                    idx[b] = ti;
+                    val[b] = tv;
+                }
+            }
+            continue;
+        }
+        if (v > val[rank - 1]) {
+            /* the new last entry, moved up past every entry it exceeds in
+             * total order (a stable re-sort of an otherwise sorted array) */
+            uint32_t b = rank - 1;
+            while (b > 0 && total_key(v) > total_key(val[b - 1])) {
+                idx[b] = idx[b - 1];
+                val[b] = val[b - 1];
+                --b;
+            }
+            idx[b] = i;
+            val[b] = v;
+        }
+    }
+    int hit = 0;
+    for (uint32_t a = 0; a < len; ++a) hit |= idx[a] == target;
+    free(idx);
+    free(val);
+    return hit;
+}
+
 /* ------------------------------------------------------------------------ */
 /* MTP acceptance                                                            */
 /* ------------------------------------------------------------------------ */

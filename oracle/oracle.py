@@ -96,6 +96,8 @@ def lib():
         L.axo_logprob_of.argtypes = [f32]
         L.axo_full_vocab_token_logprob.restype = f32
         L.axo_full_vocab_token_logprob.argtypes = [vp, u32, u32, f32]
+        L.axo_soft_close_in_top_k.restype = C.c_int
+        L.axo_soft_close_in_top_k.argtypes = [vp, u32, u32, u32]
         L.axo_mtp_accept_count.restype = u32
         L.axo_mtp_accept_count.argtypes = [
             u32, vp, vp, u32, vp, vp, vp, u32, vp, u32, vp, vp, vp, vp, u32, vp, vp, vp, u32,
@@ -277,6 +279,13 @@ def logprob_of(prob: float) -> float:
 def full_vocab_token_logprob(logits, token: int, temperature: float) -> float:
     a = _f32(logits)
     return float(lib().axo_full_vocab_token_logprob(a.ctypes.data, a.size, token, temperature))
+
+
+def soft_close_in_top_k(logits, target: int, rank: int) -> bool:
+    a = _f32(logits)
+    if a.size == 0:
+        return False
+    return bool(lib().axo_soft_close_in_top_k(a.ctypes.data, a.size, target, rank))
 
 
 def _csr(dists):

@@ -501,3 +501,41 @@ def test_mtp_first_token_follows_the_target_law(oracle, filtered):
     assert set(np.unique(first).tolist()) <= set(pid.tolist())
     chi2 = sum((np.count_nonzero(first == i) - N * q) ** 2 / (N * q) for i, q in zip(pid, pv))
     assert chi2 < 25.0, chi2  # <= 5 dof, p ~ 1e-4
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_soft_close_probe_is_a_rank_count(oracle, seed):
+    """ngram_accel.rs:1609-1640 without NaN or signed zeros: the running top
+    set replaces its last entry only on a strictly larger logit, so the final
+    set is the top `rank` by (logit desc, id asc): the target is in it iff
+    fewer than `rank` logits beat it (larger, or equal at a lower id).
+    Repeated values (bf16-like quantisation) exercise the tie rule."""
+    rng = np.random.default_rng([seed, 91])
+    for trial in range(40):
+        n = int(rng.integers(1, 300))
+        x = np.round(rng.standard_normal(n) * 2.0, int(rng.integers(0, 3))).astype(np.float32)
+        x[x == 0] = np.float32(0.25)  # no zeros: +0 and -0 compare equal but sort apart
+        rank = int(rng.integers(0, 12))
+        for t in rng.integers(0, n, 5):
+            beats = int(np.count_nonzero(x > x[t]) + np.count_nonzero(x[:t] == x[t]))
+            assert oracle.soft_close_in_top_k(x, int(t), rank) == (rank > 0 and beats < rank), (seed, trial, t)
+
+
+def test_soft_close_probe_nan_and_signed_zero(oracle):
+    """Worked by hand from the reference's loop: the first `rank` logits sort
+    by total order (+NaN above +inf, -NaN below -inf, -0 below +0), later
+    ones enter only on IEEE `>`, which no value passes against a NaN and +0
+    does not pass against -0."""
+    nan = np.float32(np.nan)
+    neg_nan = np.array([0xFFC00000], np.uint32).view(np.float32)[0]
+    assert oracle.soft_close_in_top_k([nan, 1.0, 2.0], 0, 1)
+    assert not oracle.soft_close_in_top_k([nan, 1.0, 2.0], 2, 1)
+    # -NaN sorts last and then blocks every replacement
+    assert not oracle.soft_close_in_top_k([1.0, neg_nan, 3.0], 2, 2)
+    assert oracle.soft_close_in_top_k([1.0, neg_nan, 3.0], 1, 2)
+    # a later +0 does not replace an earlier -0
+    assert oracle.soft_close_in_top_k([-0.0, 0.0], 0, 1)
+    assert not oracle.soft_close_in_top_k([-0.0, 0.0], 1, 1)
+    # +0 sorts above -0 in the first rank entries, so -0 is the one replaced
+    assert oracle.soft_close_in_top_k([0.0, -0.0, 1.0], 0, 2)
+    assert not oracle.soft_close_in_top_k([0.0, -0.0, 1.0], 1, 2)

@@ -380,3 +380,23 @@ def test_filtered_target_probability_applies_min_p(oracle):
     ids, probs = oracle.token_distribution(row, P(MlxSamplingParams.new(1.0, 1.0, 0)))
     d = dict(zip(ids.tolist(), probs.tolist()))
     assert abs(d[0] - 0.9) < 1e-5
+
+
+def test_soft_close_probe_membership_by_rank(oracle):
+    # ngram_accel.rs:1766-1776: top-3 of these logits are ids 1, 3, 2
+    logits = [0.1, 5.0, 3.0, 4.0, 0.5]
+    assert oracle.soft_close_in_top_k(logits, 1, 3)
+    assert oracle.soft_close_in_top_k(logits, 2, 3)
+    assert oracle.soft_close_in_top_k(logits, 3, 3)
+    assert not oracle.soft_close_in_top_k(logits, 0, 3)
+    assert not oracle.soft_close_in_top_k(logits, 4, 3)
+    assert oracle.soft_close_in_top_k(logits, 1, 1)
+    assert not oracle.soft_close_in_top_k(logits, 3, 1)
+
+
+def test_soft_close_probe_edge_cases(oracle):
+    # ngram_accel.rs:1778-1786
+    assert not oracle.soft_close_in_top_k([], 0, 3)
+    assert not oracle.soft_close_in_top_k([1.0, 2.0], 0, 0)
+    assert not oracle.soft_close_in_top_k([1.0, 2.0], 9, 3)
+    assert oracle.soft_close_in_top_k([1.0, 2.0], 0, 3)
