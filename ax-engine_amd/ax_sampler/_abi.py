@@ -70,6 +70,7 @@ EXPORTS = (
     "axs_mtp_verify_ex",
     "axs_token_logprob_batch",
     "axs_soft_close_probe",
+    "axs_top_logprobs",
     "axs_timing_enable",
     "axs_timing_read",
 )
@@ -206,6 +207,8 @@ def lib():
             L.axs_argmax_batch_noalloc.argtypes = [i32, vp, i32, i32, i32, i64, vp, vp, vp]
             L.axs_token_logprob_batch.restype = i32
             L.axs_token_logprob_batch.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
+            L.axs_top_logprobs.restype = i32
+            L.axs_top_logprobs.argtypes = [vp, vp, i32, i32, i32, i64, vp, i32, vp, vp, vp]
             L.axs_soft_close_probe.restype = i32
             L.axs_soft_close_probe.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
             L.axs_mtp_verify_ex.restype = i32

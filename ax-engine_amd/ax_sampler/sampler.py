@@ -387,6 +387,23 @@ class HipSampler:
                                                   out.data_ptr(), self._stream(stream)))
         return out
 
+    def top_logprobs(self, logits, temperatures, n: int, stream=None):
+        """The n largest full-softmax probabilities per row with their
+        full_vocab_token_logprob (axs_top_logprobs): (ids int32 [B, n] holding
+        uint32 ids, logprobs f32 [B, n]) on the device."""
+        torch = _torch()
+        if logits.stride(1) != 1:
+            logits = logits.contiguous()
+        B, V = logits.shape
+        tem = temperatures if isinstance(temperatures, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(np.asarray(temperatures, dtype=np.float32))).to(self.device)
+        ids = torch.empty((B, n), dtype=torch.int32, device=self.device)
+        lp = torch.empty((B, n), dtype=torch.float32, device=self.device)
+        _abi.check(self.L.axs_top_logprobs(self.ctx, logits.data_ptr(), _dtype_code(logits), B, V,
+                                           logits.stride(0), tem.data_ptr(), n, ids.data_ptr(),
+                                           lp.data_ptr(), self._stream(stream)))
+        return ids, lp
+
     def soft_close_probe(self, logits, think_ids, ranks, stream=None):
         """think_soft_close_in_top_k per row (axs_soft_close_probe): 1 when
         think_ids[r] is within the top ranks[r] raw logits of row r, else 0

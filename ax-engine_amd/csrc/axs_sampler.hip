@@ -176,6 +176,11 @@ struct KArgs {
     // and temperature of each row; the row's law is the untruncated softmax
     const uint32_t* lp_tokens;
     const float* lp_temps;
+    // top-N rows (axs_top_logprobs): topn > 0 lists each row's n largest
+    // full-softmax probabilities instead of one token's
+    uint32_t topn;
+    uint32_t* topn_ids;  // [rows, topn]
+    float* topn_lp;      // [rows, topn]
     // MTP verify options (axs_mtp_verify_ex); mtp_stream: uniforms in the
     // reference's stream order (else the slot layout of axs_mtp_verify)
     const uint32_t* mtp_sources;  // [batch, depth] or NULL
@@ -1051,7 +1056,29 @@ __device__ __forceinline__ bool finish_decide(const KArgs& a, int r, const axs_s
         const uint32_t t = a.lp_tokens[r];
         const bool direct = t >= (uint32_t)a.vocab || mode == M_GREEDY || !isfinite(m) ||
                             !isfinite(__fdiv_rn(1.0f, p.temperature));
-        if (direct) {
+        if (a.topn) {
+            // top-N rows: T <= 0 lists the first maximum (0); no finite
+            // maximum or temperature makes every p 0 (ids in order, -30)
+            if (mode == M_GREEDY || !isfinite(m) || !isfinite(__fdiv_rn(1.0f, p.temperature))) {
+                for (uint32_t k = (uint32_t)tid; k < a.topn; k += (uint32_t)NT) {
+                    uint32_t id = NONE;
+                    float lp = -INFINITY;
+                    if (mode == M_GREEDY) {
+                        if (k == 0) {
+                            id = am;
+                            lp = 0.0f;
+                        }
+                    } else if (k < (uint32_t)a.vocab) {
+                        id = k;
+                        lp = -30.0f;
+                    }
+                    a.topn_ids[(size_t)r * a.topn + k] = id;
+                    a.topn_lp[(size_t)r * a.topn + k] = lp;
+                }
+                if (tid == 0) write_row(a, r, 0u, 0.0f, AXS_FLAG_EXACT_PATH);
+                return false;
+            }
+        } else if (direct) {
             if (tid == 0) {
                 float lp = -30.0f;
                 if (t < (uint32_t)a.vocab && mode == M_GREEDY) lp = am == t ? 0.0f : -INFINITY;
@@ -3550,6 +3577,111 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     __threadfence_block();
     __syncthreads();  // every S store complete before the decisions read S
 
+    if (a.lp_tokens && a.topn) {
+        // top-N row: the n largest p (ties to the lower id) by a radix
+        // select of the N-th largest p's bit pattern (4 passes of 8 bits over
+        // the dense row; p >= 0, so the bits order as the values), those
+        // above it and the lowest ids equal to it gathered, one wave's rank
+        // sort; each with max(ln(max(p / S, 1e-37)), -30)
+        const uint32_t n = a.topn < V ? a.topn : V;
+        uint32_t* hist = s_cnt;            // 256 bins
+        uint32_t* sel = s_cnt + 256;       // up to 64 selected ids
+        uint32_t* eq = s_cnt + 512;        // ids equal to the cut, up to EQCAP
+        constexpr uint32_t EQCAP = 4096;
+        uint32_t prefix = 0, mask = 0, want = n;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (uint32_t i = tid; i < 256u; i += NT_EX) hist[i] = 0;
+            __syncthreads();
+            for (uint32_t i = tid; i < V; i += NT_EX) {
+                const uint32_t b = __float_as_uint(dense[i]);
+                if ((b & mask) == prefix) atomicAdd(&hist[(b >> shift) & 255u], 1u);
+            }
+            __syncthreads();
+            if (tid == 0) {
+                uint32_t cum = 0, d = 0;
+                for (int q = 255; q >= 0; --q) {
+                    if (cum + hist[q] >= want) {
+                        d = (uint32_t)q;
+                        break;
+                    }
+                    cum += hist[q];
+                }
+                s_k = d;
+                s_cross = want - cum;
+            }
+            __syncthreads();
+            prefix |= s_k << shift;
+            mask |= 255u << shift;
+            want = s_cross;
+            __syncthreads();
+        }
+        // prefix: the N-th largest p; want: how many of its copies are listed
+        if (tid == 0) {
+            s_k = 0;     // ids above the cut
+            s_cross = 0; // ids equal to it
+        }
+        __syncthreads();
+        for (uint32_t i = tid; i < V; i += NT_EX) {
+            const uint32_t b = __float_as_uint(dense[i]);
+            if (b > prefix) sel[atomicAdd(&s_k, 1u)] = i;
+            else if (b == prefix) {
+                const uint32_t q = atomicAdd(&s_cross, 1u);
+                if (q < EQCAP) eq[q] = i;
+            }
+        }
+        __syncthreads();
+        const uint32_t ngt = s_k, neq = s_cross;
+        if (neq <= EQCAP) {
+            // the `want` lowest ids among the copies: rank = smaller ids
+            for (uint32_t q = tid; q < neq; q += NT_EX) {
+                const uint32_t id = eq[q];
+                uint32_t rk = 0;
+                for (uint32_t j = 0; j < neq; ++j) rk += eq[j] < id ? 1u : 0u;
+                if (rk < want) sel[ngt + rk] = id;
+            }
+        } else {
+            // very many copies: the lowest ids one at a time
+            uint32_t last = 0;
+            for (uint32_t k = 0; k < want; ++k) {
+                uint32_t best = NONE;
+                for (uint32_t i = tid; i < V; i += NT_EX)
+                    if (__float_as_uint(dense[i]) == prefix && (k == 0 || i > last) && i < best) best = i;
+                if (tid == 0) s_k = NONE;
+                __syncthreads();
+                atomicMin(&s_k, best);
+                __syncthreads();
+                last = s_k;
+                if (tid == 0) sel[ngt + k] = last;
+                __syncthreads();
+            }
+        }
+        __threadfence_block();
+        __syncthreads();
+        if (tid < 64) {
+            // (p desc, id asc): each lane's entry goes to its rank
+            const float F0 = S[V - 1];
+            const bool okF = F0 > 0.0f && isfinite(F0);
+            const uint32_t id = (uint32_t)tid < n ? sel[tid] : 0u;
+            const float pv = (uint32_t)tid < n ? dense[id] : 0.0f;
+            const uint64_t key = (uint32_t)tid < n ? (((uint64_t)__float_as_uint(pv) << 32) | (uint32_t)~id) : 0ull;
+            uint32_t rk = 0;
+            for (uint32_t j = 0; j < n; ++j) {
+                const uint64_t kj = ((uint64_t)(uint32_t)__shfl((int)(uint32_t)(key >> 32), (int)j, 64) << 32) |
+                                    (uint32_t)__shfl((int)(uint32_t)key, (int)j, 64);
+                rk += kj > key ? 1u : 0u;
+            }
+            if ((uint32_t)tid < n) {
+                a.topn_ids[(size_t)r * a.topn + rk] = id;
+                a.topn_lp[(size_t)r * a.topn + rk] = okF ? logprob_of(__fdiv_rn(pv, F0)) : -30.0f;
+            }
+            for (uint32_t k = n + (uint32_t)tid; k < a.topn; k += 64u) {
+                a.topn_ids[(size_t)r * a.topn + k] = NONE;
+                a.topn_lp[(size_t)r * a.topn + k] = -INFINITY;
+            }
+            if (tid == 0) write_row(a, r, 0u, 0.0f, AXS_FLAG_EXACT_PATH);
+        }
+        return;
+    }
     if (a.lp_tokens) {
         // token-logprob row: max(ln(max(p_t / S, 1e-37)), -30) with S the
         // index-order f32 sum (crates/ax-engine-mlx/src/sampling.rs:772-786)
@@ -4990,6 +5122,42 @@ int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int
     a.lp_temps = temperatures;
     a.out_ids = ctx->mtp_tok;  // the rows' tokens echoed: scratch
     a.out_lp = out_logprob;
+    Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
+    if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
+    return order_end(ctx, s);
+}
+
+int axs_top_logprobs(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
+                     int64_t row_stride, const float* temperatures, int n, uint32_t* out_ids, float* out_logprob,
+                     void* stream) {
+    if (!ctx || !logits || !temperatures || !out_ids || !out_logprob)
+        return fail(AXS_E_INVALID, "ctx, logits, temperatures, out_ids and out_logprob must be non-NULL");
+    if (dtype != AXS_DTYPE_F32 && dtype != AXS_DTYPE_BF16) return fail(AXS_E_INVALID, "bad dtype");
+    if (batch < 1 || vocab < 1 || row_stride < vocab) return fail(AXS_E_INVALID, "bad shape");
+    if (n < 1 || n > AXS_TOP_LOGPROBS_MAX) return fail(AXS_E_INVALID, "n must be 1..AXS_TOP_LOGPROBS_MAX");
+    if (batch > ctx->max_rows || vocab > ctx->max_vocab)
+        return fail(AXS_E_CAPACITY, "batch or vocab larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DevGuard g(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = order_begin(ctx, s);
+    if (rc) return rc;
+    // the rows' token list (unused by top-N rows): zeros
+    hipLaunchKernelGGL(k_fill_u32, dim3((batch + 255) / 256), dim3(256), 0, s, ctx->lp_tok, (uint32_t)batch, 0u);
+    AXS_HIP_CHECK(hipGetLastError());
+    KArgs a{};
+    a.logits = logits;
+    a.dtype = dtype;
+    a.nrows = batch;
+    a.vocab = vocab;
+    a.stride = row_stride;
+    a.params = nullptr;
+    a.lp_tokens = ctx->lp_tok;
+    a.lp_temps = temperatures;
+    a.topn = (uint32_t)n;
+    a.topn_ids = out_ids;
+    a.topn_lp = out_logprob;
+    a.out_ids = ctx->mtp_tok;  // scratch
     Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
     if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
     return order_end(ctx, s);

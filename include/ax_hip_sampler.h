@@ -355,6 +355,21 @@ int axs_token_logprob_batch(axs_context* ctx, const void* logits, int dtype, int
                             int64_t row_stride, const uint32_t* tokens, const float* temperatures,
                             float* out_logprob, void* stream);
 
+/* Top-N log-probabilities per row: the n (1..AXS_TOP_LOGPROBS_MAX) ids with
+ * the largest full-softmax probability exp((l - max) / T) (non-finite as
+ * 0; ties to the lower id), in that order, each with
+ * full_vocab_token_logprob (crates/ax-engine-mlx/src/sampling.rs:761-787;
+ * the same value axs_token_logprob_batch returns for the id).  The
+ * reference's server rejects top_logprobs
+ * (crates/ax-engine-server/src/openai/requests.rs:1283-1298): this is a
+ * build extension over its sampled-token logprob.  T <= 0 lists the first
+ * maximum (0) only; slots past it or past vocab hold AXS_NONE_U32 / -inf.
+ * temperatures [batch], out_ids and out_logprob [batch, n]: device arrays. */
+#define AXS_TOP_LOGPROBS_MAX 64
+int axs_top_logprobs(axs_context* ctx, const void* logits, int dtype, int batch, int vocab,
+                     int64_t row_stride, const float* temperatures, int n, uint32_t* out_ids, float* out_logprob,
+                     void* stream);
+
 /* Think soft-close rank probe, per row: out_hit[r] = 1 when think_ids[r]
  * sits within the top ranks[r] raw logits of row r (no processors, no
  * temperature), else 0 — think_soft_close_in_top_k

@@ -822,6 +822,52 @@ float axo_full_vocab_token_logprob(const float* logits, uint32_t n, uint32_t tok
     return fmaxf(logf(fmaxf(unnorm / sum, 1e-37f)), -30.0f);
 }
 
+/* Top-N log-probabilities (a build extension over full_vocab_token_logprob,
+ * sampling.rs:761-787; the reference's server rejects top_logprobs,
+ * crates/ax-engine-server/src/openai/requests.rs:1283-1298): the n ids with
+ * the largest unnormalised p = exp((l - max) / T) (non-finite p as 0), ties
+ * to the lower id, each with full_vocab_token_logprob.  T <= 0 lists only
+ * the first maximum (log-probability 0); unused slots hold id 0xFFFFFFFF and
+ * -inf. */
+typedef struct { float p; uint32_t id; } topn_ent;
+
+static int topn_cmp(const void* a, const void* b) {
+    const topn_ent* x = (const topn_ent*)a;
+    const topn_ent* y = (const topn_ent*)b;
+    if (x->p != y->p) return x->p > y->p ? -1 : 1;
+    return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
+}
+
+void axo_top_logprobs(const float* logits, uint32_t V, float temperature, uint32_t n, uint32_t* out_ids,
+                      float* out_lp) {
+    for (uint32_t k = 0; k < n; ++k) {
+        out_ids[k] = 0xFFFFFFFFu;
+        out_lp[k] = -INFINITY;
+    }
+    if (V == 0 || n == 0) return;
+    if (temperature <= 0.0f) {
+        out_ids[0] = axo_argmax_f32(logits, V);
+        out_lp[0] = 0.0f;
+        return;
+    }
+    float inv = 1.0f / temperature;
+    float m = -INFINITY;
+    for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, logits[i]);
+    topn_ent* e = (topn_ent*)malloc(sizeof(topn_ent) * V);
+    for (uint32_t i = 0; i < V; ++i) {
+        float q = expf((logits[i] - m) * inv);
+        e[i].p = isfinite(q) ? q : 0.0f;
+        e[i].id = i;
+    }
+    qsort(e, V, sizeof(topn_ent), topn_cmp);
+    uint32_t k_n = n < V ? n : V;
+    for (uint32_t k = 0; k < k_n; ++k) {
+        out_ids[k] = e[k].id;
+        out_lp[k] = axo_full_vocab_token_logprob(logits, V, e[k].id, temperature);
+    }
+    free(e);
+}
+
 /* think_soft_close_in_top_k (crates/ax-engine-mlx/src/ngram_accel.rs:1609-1640):
  * the reference's single pass, kept literally: the first `rank` logits taken
  * as they come and stably sorted descending by total order (f32::total_cmp);

@@ -96,6 +96,8 @@ def lib():
         L.axo_logprob_of.argtypes = [f32]
         L.axo_full_vocab_token_logprob.restype = f32
         L.axo_full_vocab_token_logprob.argtypes = [vp, u32, u32, f32]
+        L.axo_top_logprobs.restype = None
+        L.axo_top_logprobs.argtypes = [vp, u32, f32, u32, vp, vp]
         L.axo_soft_close_in_top_k.restype = C.c_int
         L.axo_soft_close_in_top_k.argtypes = [vp, u32, u32, u32]
         L.axo_mtp_accept_count.restype = u32
@@ -279,6 +281,16 @@ def logprob_of(prob: float) -> float:
 def full_vocab_token_logprob(logits, token: int, temperature: float) -> float:
     a = _f32(logits)
     return float(lib().axo_full_vocab_token_logprob(a.ctypes.data, a.size, token, temperature))
+
+
+def top_logprobs(logits, temperature: float, n: int):
+    """(ids uint32[n], logprobs f32[n]): the n largest full-softmax
+    probabilities, ties to the lower id, with full_vocab_token_logprob."""
+    a = _f32(logits)
+    ids = np.zeros(max(n, 1), np.uint32)
+    lp = np.zeros(max(n, 1), np.float32)
+    lib().axo_top_logprobs(a.ctypes.data, a.size, temperature, n, ids.ctypes.data, lp.ctypes.data)
+    return ids[:n], lp[:n]
 
 
 def soft_close_in_top_k(logits, target: int, rank: int) -> bool:

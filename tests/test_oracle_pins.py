@@ -539,3 +539,35 @@ def test_soft_close_probe_nan_and_signed_zero(oracle):
     # +0 sorts above -0 in the first rank entries, so -0 is the one replaced
     assert oracle.soft_close_in_top_k([0.0, -0.0, 1.0], 0, 2)
     assert not oracle.soft_close_in_top_k([0.0, -0.0, 1.0], 1, 2)
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_top_logprobs_follow_full_vocab_token_logprob(oracle, seed):
+    """The top-N list is the full_vocab_token_logprob ranking: with every
+    listed log-probability above the -30 clamp, the ids are the first n of
+    all ids ordered by (log-probability desc, id asc) — log-probabilities
+    from the function pinned by its closed form above — and the values are
+    that function's.  Repeated logits exercise the lower-id tie rule."""
+    rng = np.random.default_rng([seed, 17])
+    for trial in range(6):
+        V = int(rng.integers(1, 400))
+        x = np.round(rng.standard_normal(V) * 2.0, 1).astype(np.float32)
+        T = float(rng.choice([0.5, 1.0, 1.7]))
+        n = int(rng.integers(1, 25))
+        ids, lp = oracle.top_logprobs(x, T, n)
+        full = np.array([oracle.full_vocab_token_logprob(x, i, T) for i in range(V)], np.float32)
+        order = np.lexsort((np.arange(V), -full))
+        k = min(n, V)
+        if full[order[k - 1]] > -30.0:
+            assert ids[:k].tolist() == order[:k].tolist(), (seed, trial)
+        assert np.array_equal(lp[:k], full[ids[:k]])
+        assert np.all(ids[k:] == 0xFFFFFFFF) and np.all(np.isneginf(lp[k:]))
+
+
+def test_top_logprobs_edge_cases(oracle):
+    x = np.array([1.0, 3.0, 3.0, -np.inf, np.nan], np.float32)
+    ids, lp = oracle.top_logprobs(x, 0.0, 3)  # T <= 0: the first maximum only
+    assert ids.tolist() == [1, 0xFFFFFFFF, 0xFFFFFFFF] and lp[0] == 0.0
+    ids, lp = oracle.top_logprobs(x, 1.0, 5)  # ties to the lower id; p(NaN) = p(-inf) = 0
+    assert ids.tolist() == [1, 2, 0, 3, 4]
+    assert lp[3] == -30.0 and lp[4] == -30.0
