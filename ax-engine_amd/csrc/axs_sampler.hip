@@ -1853,18 +1853,23 @@ constexpr uint32_t RERR_CAP = 4u;          // more than CAPP captures
 constexpr uint32_t NMIXW = NBUCKET / 32;
 constexpr uint32_t NTAILB = 5120;                  // tail buckets: p in [2^-24, 2^-14)
 constexpr uint32_t BEND_STRIDE = NBUCKET + NTAILB;  // per row: bucket ends, top-value counts
+// LDS state of block_exact_sums
+struct SumLds {
+    Xd w[NT_EX / 64];
+    float s;
+    uint32_t cross, npc;
+    uint32_t pc[32];  // predicted crossings of a tile
+};
+
 struct ExLds {
     uint32_t cnt[NBUCKET];  // bucket counts, then bucket ends; then sort scratch
     uint64_t stage[(NT_EX / 64) * 128];  // each wave's window of keys
     uint32_t mixed[NMIXW];  // buckets of more than 64 keys with two different p
     uint32_t topv[NMIXW];   // tail buckets holding their top value
     uint32_t done[NMIXW];   // tail buckets sorted and summed element by element
-    Xd w[NT_EX / 64];
     uint32_t u[NT_EX / 64];
-    float s;
     uint32_t k, cross, err, xc;
-    uint32_t npc;             // predicted crossings of the tile
-    uint32_t pc[32];          // ... their positions
+    SumLds sum;  // the exact running sums' state
 };
 
 struct RowLds {
@@ -3032,6 +3037,149 @@ __device__ __forceinline__ uint32_t bucket_of(uint64_t key) {
     return b < NBUCKET ? b : NBUCKET - 1;
 }
 
+// Exact running sums S[k] = fl(S[k-1] + X(k)) over positions [k0, kend) from
+// the sum s0, by the NT_EX threads of one workgroup (axs_exact_sum.h); S may
+// be null when only the last sum is wanted.  Returns the last sum (every
+// thread).  A range of up to 256 terms is summed by the reference's own loop
+// on one thread (loads issued eight at a time: cheaper than the scan's
+// barriers).  Otherwise a tile of IT terms per thread is loaded once; a scan
+// adds the terms in the binade of the current sum, and the first term that
+// would leave it (the earliest crossing over the block) is added directly by
+// its thread; the rest of the tile is scanned again in the new binade.  Each
+// scan covers a window of the tile that ends a margin after the next
+// position where the real-valued prefix sum (fixed point, 2^-40) passes a
+// power of two: the rounded sum crosses there or close by, and a window
+// without a crossing only means one more scan.  The barriers are LDS-only:
+// S is read only after the call.
+template <uint32_t IT, typename XF>
+__device__ float block_exact_sums(XF X, uint32_t k0, uint32_t kend, float s0, float* S, SumLds& L) {
+    constexpr uint32_t WMARGIN = 128;
+    const int tid = threadIdx.x;
+    if (kend - k0 <= 256u) {
+        if (tid == 0) {
+            float s = s0;
+            for (uint32_t i0 = k0; i0 < kend; i0 += 8u) {
+                float xv[8];
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j) xv[j] = i0 + j < kend ? X(i0 + j) : 0.0f;
+#pragma unroll
+                for (uint32_t j = 0; j < 8u; ++j)
+                    if (i0 + j < kend) {
+                        s = __fadd_rn(s, xv[j]);
+                        if (S) S[i0 + j] = s;
+                    }
+            }
+            L.s = s;
+        }
+        __threadfence_block();
+        __syncthreads();
+        const float fin = L.s;
+        __syncthreads();
+        return fin;
+    }
+    if (tid == 0) L.cross = NONE;
+    __syncthreads();
+    float s = s0;
+    for (uint32_t k = k0; k < kend;) {
+        const uint32_t tile = min((uint32_t)NT_EX * IT, kend - k);
+        const uint32_t i0 = k + (uint32_t)tid * IT;
+        float xv[IT];
+#pragma unroll
+        for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
+        // predicted crossings: the real prefix from the tile's start sum
+        {
+            uint64_t loc = 0;
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) loc += (uint64_t)((double)xv[j] * 0x1p40);
+            Xd fx = xd_identity();
+            fx.inc0 = fx.inc1 = loc;
+            const uint64_t rb = block_excl_scan_xd<NT_EX>(fx, L.w).inc0;
+            if (tid == 0) L.npc = 0;
+            lds_barrier();
+            double rs = (double)s + (double)rb * 0x1p-40;
+            int eprev = ilogb(rs > 0.0 ? rs : 0x1p-1000);
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) {
+                if (i0 + j >= k + tile) continue;
+                rs += (double)(uint64_t)((double)xv[j] * 0x1p40) * 0x1p-40;
+                const int e = ilogb(rs > 0.0 ? rs : 0x1p-1000);
+                if (e > eprev) {
+                    const uint32_t slot = atomicAdd(&L.npc, 1u);
+                    if (slot < 32u) L.pc[slot] = i0 + j;
+                }
+                eprev = e;
+            }
+            lds_barrier();
+        }
+        const uint32_t npc = min(L.npc, 32u);
+        uint32_t kk = k;  // the tile's first term not yet added
+        while (true) {
+            // the window [kk, we)
+            uint32_t nxt = NONE;
+            for (uint32_t q = 0; q < npc; ++q) {
+                const uint32_t pq = L.pc[q];
+                if (pq >= kk && pq < nxt) nxt = pq;
+            }
+            const uint32_t we = nxt == NONE ? k + tile : min(k + tile, nxt + 1u + WMARGIN);
+            const Binade bd = binade_of(s);
+            Term t[IT];
+            Xd mine = xd_identity();
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) {
+                t[j].c0 = t[j].c1 = 0u;
+                if (i0 + j >= kk && i0 + j < we) {
+                    t[j] = term_of(xv[j], bd.E);
+                    mine = xd_compose(mine, xd_of(t[j]));
+                }
+            }
+            Xd pre = block_excl_scan_xd<NT_EX>(mine, L.w);
+            const uint32_t b0 = bd.A & 1u;
+            uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
+            uint32_t par = b0 ? pre.par1 : pre.par0;
+            uint32_t mycross = NONE;
+            float xs = 0.0f, last = 0.0f;
+#pragma unroll
+            for (uint32_t j = 0; j < IT; ++j) {
+                const uint32_t i = i0 + j;
+                if (i < kk || i >= we || mycross != NONE) continue;
+                const uint32_t cc = par ? t[j].c1 : t[j].c0;
+                if (acc + cc >= (1ull << 24)) {
+                    mycross = i;
+                    xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
+                    continue;
+                }
+                acc += cc;
+                par = (uint32_t)(acc & 1u);
+                last = binade_value((uint32_t)acc, bd.E);
+                if (S) S[i] = last;
+            }
+            if (mycross != NONE) atomicMin(&L.cross, mycross);
+            lds_barrier();
+            const uint32_t kc = L.cross;
+            if (kc == NONE) {
+                if (we - 1u - i0 < IT) L.s = last;  // this thread holds the window's last term
+            } else if (mycross == kc) {
+                if (S) S[kc] = xs;
+                L.s = xs;
+            }
+            lds_barrier();
+            s = L.s;  // rewritten only after the next scan's barriers
+            if (kc == NONE) {
+                kk = we;
+            } else {
+                if (tid == 0) L.cross = NONE;  // read by every thread before the barrier above
+                kk = kc + 1u;
+            }
+            if (kk >= k + tile) break;
+        }
+        k += tile;
+        lds_barrier();  // L.pc read by every thread before the next tile rewrites it
+    }
+    __threadfence_block();
+    __syncthreads();
+    return s;
+}
+
 // Buckets of p >= 2^-14 (bucket 7168 holds 2^-14 itself) are the head:
 // sorted and summed element by element.  The tail buckets [NHB, TB_END)
 // (2^-24 <= p < 2^-14) hold one binade each except for a power-of-two top
@@ -3053,9 +3201,9 @@ __device__ __forceinline__ uint32_t bucket_top(uint32_t b) { return 0x3F800000u 
 template <uint32_t XI>
 __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState& rs, ExLds& XL) {
     uint32_t* s_cnt = XL.cnt;
-    Xd* s_w = XL.w;
+    Xd* s_w = XL.sum.w;
     uint32_t* s_u = XL.u;
-    float& s_s = XL.s;
+    float& s_s = XL.sum.s;
     uint32_t &s_k = XL.k, &s_cross = XL.cross, &s_err = XL.err;
     const int tid = threadIdx.x;
     const axs_sampling_params p = row_params(a, r);
@@ -3257,147 +3405,11 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     }
     __syncthreads();
 
-    // exact running sums S[k] = fl(S[k-1] + x_k), in parallel (axs_exact_sum.h),
-    // over positions [k0, kend) of the terms pdesc_p(kp[k]) (dense[k] without
-    // kp) from the sum s0; returns the last sum.  Whole block.
-    // A tile of IT terms per thread is loaded once; a scan adds the terms in
-    // the binade of the current sum, and the first term that would leave it
-    // (the earliest crossing over the block) is added directly by its
-    // thread; the rest of the tile is scanned again in the new binade.  Each
-    // scan covers a window of the tile that ends a margin after the next
-    // position where the real-valued prefix sum (fixed point, 2^-40) passes a
-    // power of two: the rounded sum crosses there or close by, and a window
-    // without a crossing only means one more scan.  The barriers are
-    // LDS-only: S is read only after the loop.
+    // exact running sums of the keys' p (or the dense row), in parallel
     constexpr uint32_t IT = XI;
-    constexpr uint32_t WMARGIN = 128;
     auto elem_sums = [&](const uint64_t* kp, uint32_t k0, uint32_t kend, float s0) -> float {
-        auto X = [&](uint32_t i) -> float { return kp ? pdesc_p(kp[i]) : dense[i]; };
-        if (kend - k0 <= 256u) {
-            // a short range: the reference's own loop on one thread, its
-            // loads issued eight at a time (cheaper than the scan's barriers)
-            if (tid == 0) {
-                float s = s0;
-                for (uint32_t i0 = k0; i0 < kend; i0 += 8u) {
-                    float xv[8];
-#pragma unroll
-                    for (uint32_t j = 0; j < 8u; ++j) xv[j] = i0 + j < kend ? X(i0 + j) : 0.0f;
-#pragma unroll
-                    for (uint32_t j = 0; j < 8u; ++j)
-                        if (i0 + j < kend) {
-                            s = __fadd_rn(s, xv[j]);
-                            S[i0 + j] = s;
-                        }
-                }
-                s_s = s;
-            }
-            __threadfence_block();
-            __syncthreads();
-            const float fin = s_s;
-            __syncthreads();
-            return fin;
-        }
-        if (tid == 0) s_cross = NONE;
-        __syncthreads();
-        float s = s0;
-        for (uint32_t k = k0; k < kend;) {
-            const uint32_t tile = min((uint32_t)NT_EX * IT, kend - k);
-            const uint32_t i0 = k + (uint32_t)tid * IT;
-            float xv[IT];
-#pragma unroll
-            for (uint32_t j = 0; j < IT; ++j) xv[j] = i0 + j < k + tile ? X(i0 + j) : 0.0f;
-            // predicted crossings: the real prefix from the tile's start sum
-            {
-                uint64_t loc = 0;
-#pragma unroll
-                for (uint32_t j = 0; j < IT; ++j) loc += (uint64_t)((double)xv[j] * 0x1p40);
-                Xd fx = xd_identity();
-                fx.inc0 = fx.inc1 = loc;
-                const uint64_t rb = block_excl_scan_xd<NT_EX>(fx, s_w).inc0;
-                if (tid == 0) XL.npc = 0;
-                lds_barrier();
-                double rs = (double)s + (double)rb * 0x1p-40;
-                int eprev = ilogb(rs > 0.0 ? rs : 0x1p-1000);
-#pragma unroll
-                for (uint32_t j = 0; j < IT; ++j) {
-                    if (i0 + j >= k + tile) continue;
-                    rs += (double)(uint64_t)((double)xv[j] * 0x1p40) * 0x1p-40;
-                    const int e = ilogb(rs > 0.0 ? rs : 0x1p-1000);
-                    if (e > eprev) {
-                        const uint32_t slot = atomicAdd(&XL.npc, 1u);
-                        if (slot < 32u) XL.pc[slot] = i0 + j;
-                    }
-                    eprev = e;
-                }
-                lds_barrier();
-            }
-            const uint32_t npc = min(XL.npc, 32u);
-            uint32_t kk = k;  // the tile's first term not yet added
-            while (true) {
-                // the window [kk, we)
-                uint32_t nxt = NONE;
-                for (uint32_t q = 0; q < npc; ++q) {
-                    const uint32_t pq = XL.pc[q];
-                    if (pq >= kk && pq < nxt) nxt = pq;
-                }
-                const uint32_t we = nxt == NONE ? k + tile : min(k + tile, nxt + 1u + WMARGIN);
-                const Binade bd = binade_of(s);
-                Term t[IT];
-                Xd mine = xd_identity();
-#pragma unroll
-                for (uint32_t j = 0; j < IT; ++j) {
-                    t[j].c0 = t[j].c1 = 0u;
-                    if (i0 + j >= kk && i0 + j < we) {
-                        t[j] = term_of(xv[j], bd.E);
-                        mine = xd_compose(mine, xd_of(t[j]));
-                    }
-                }
-                Xd pre = block_excl_scan_xd<NT_EX>(mine, s_w);
-                const uint32_t b0 = bd.A & 1u;
-                uint64_t acc = (uint64_t)bd.A + (b0 ? pre.inc1 : pre.inc0);
-                uint32_t par = b0 ? pre.par1 : pre.par0;
-                uint32_t mycross = NONE;
-                float xs = 0.0f, last = 0.0f;
-#pragma unroll
-                for (uint32_t j = 0; j < IT; ++j) {
-                    const uint32_t i = i0 + j;
-                    if (i < kk || i >= we || mycross != NONE) continue;
-                    const uint32_t cc = par ? t[j].c1 : t[j].c0;
-                    if (acc + cc >= (1ull << 24)) {
-                        mycross = i;
-                        xs = __fadd_rn(binade_value((uint32_t)acc, bd.E), xv[j]);  // the direct add
-                        continue;
-                    }
-                    acc += cc;
-                    par = (uint32_t)(acc & 1u);
-                    last = binade_value((uint32_t)acc, bd.E);
-                    S[i] = last;
-                }
-                if (mycross != NONE) atomicMin(&s_cross, mycross);
-                lds_barrier();
-                const uint32_t kc = s_cross;
-                if (kc == NONE) {
-                    if (we - 1u - i0 < IT) s_s = last;  // this thread holds the window's last term
-                } else if (mycross == kc) {
-                    S[kc] = xs;
-                    s_s = xs;
-                }
-                lds_barrier();
-                s = s_s;  // rewritten only after the next scan's barriers
-                if (kc == NONE) {
-                    kk = we;
-                } else {
-                    if (tid == 0) s_cross = NONE;  // read by every thread before the barrier above
-                    kk = kc + 1u;
-                }
-                if (kk >= k + tile) break;
-            }
-            k += tile;
-            lds_barrier();  // XL.pc read by every thread before the next tile rewrites it
-        }
-        __threadfence_block();
-        __syncthreads();
-        return s;
+        if (kp) return block_exact_sums<IT>([&](uint32_t i) { return pdesc_p(kp[i]); }, k0, kend, s0, S, XL.sum);
+        return block_exact_sums<IT>([&](uint32_t i) { return dense[i]; }, k0, kend, s0, S, XL.sum);
     };
     // tail bucket b extracted to its range of keys, sorted, and summed element
     // by element from the sum before it (whole block, once per bucket)
