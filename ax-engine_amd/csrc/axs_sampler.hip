@@ -69,6 +69,10 @@ constexpr uint32_t BIAS_LDS = 256;    // bias entries per chunk
 constexpr uint32_t KEPT_CAP = 2048;   // kept entries per MTP distribution row
 constexpr uint32_t BIG_LDS_SORT = 4096;
 constexpr float P_FLOOR = 0x1p-24f;   // smaller terms never change a sum >= 1
+// RowState.flags of an MTP pipeline row whose kept list stays in the row's
+// buffers (sorted keys, or the dense row's p > 0 entries): too long for the
+// KEPT_CAP lists.  Internal: never an output flag.
+constexpr uint32_t RSF_LIST_IN_ROW = 1u << 30;
 
 // chunk-stat flags
 constexpr uint32_t CS_OVERFLOW = 1u;
@@ -3871,7 +3875,9 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         // bucket of more than 64 keys with a single p is still in arbitrary
         // id order, so each one holding such a position is sorted first
         const uint32_t po = (a.out_kept && a.out_kept_cap > 0) ? min(Lk, (uint32_t)a.out_kept_cap) : 0u;
-        const uint32_t pw = a.ws_kept_id ? min(Lk, KEPT_CAP) : 0u;
+        // an MTP row's whole kept list is put in order: listed below when it
+        // is short, read in place by the verify kernel otherwise
+        const uint32_t pw = a.ws_kept_id ? Lk : 0u;
         const uint32_t P = max(po, pw);
         const uint64_t kj0 = key_at(j);  // a tail bucket read here is extracted and sorted
         if (P > n_head && !tail_all) tail_sort_all();
@@ -3913,7 +3919,7 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         const uint32_t ne = kept < cap ? kept : cap;
         for (uint32_t i = tid; i < ne; i += NT_EX) a.out_kept[(size_t)r * cap + i] = i < nw ? pdesc_id(keys[i]) : NONE;
     }
-    const uint32_t nws = Lk < KEPT_CAP ? Lk : KEPT_CAP;
+    const uint32_t nws = Lk <= KEPT_CAP ? Lk : 0u;
     if (sorted && a.ws_kept_id)
         for (uint32_t i = tid; i < nws; i += NT_EX) {
             a.ws_kept_id[(size_t)r * KEPT_CAP + i] = pdesc_id(keys[i]);
@@ -3924,21 +3930,29 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
     if (a.out_kept_count) a.out_kept_count[r] = kept;
     if (a.ws_kept_id) {
         uint32_t o = 0;
+        uint32_t rsf = 0;
         if (sorted) {
             o = nws;
             // ids below 2^-24 never carry normalised mass ≥ one f32 ulp of 1, but
             // they are entries of the reference's distribution: refuse to
             // truncate silently
             if (kept > Lk) flags |= AXS_FLAG_ERROR;
+            if (Lk > KEPT_CAP) {  // the list is the row's sorted keys [0, Lk)
+                o = Lk;
+                rsf = RSF_LIST_IN_ROW;
+            }
         } else {
             o = dlist;
             kept = dpos;  // an MTP distribution counts its p > 0 entries
+            if (dpos > KEPT_CAP) {  // the list is the dense row's p > 0 entries
+                o = dpos;
+                rsf = RSF_LIST_IN_ROW;
+            }
         }
-        if (kept > KEPT_CAP) flags |= AXS_FLAG_ERROR;
         a.rstate[r].kept = kept;
         a.rstate[r].nlist = o;
         a.rstate[r].F = F;
-        a.rstate[r].flags = flags;
+        a.rstate[r].flags = flags | rsf;
     }
 }
 
@@ -3987,6 +4001,7 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
     __shared__ float s_rsum, s_total;
     __shared__ uint32_t s_cr;
     __shared__ uint64_t s_mx;
+    __shared__ SumLds s_sum;
     __shared__ uint32_t s_corr;
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
@@ -4044,14 +4059,35 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
             s_fd = -1;
         }
         __syncthreads();
-        for (uint32_t k = tid; k < rt.nlist; k += NT_MTP)
-            if (tid_l[k] == d) atomicMax(&s_ft, (int)k);
-        if (has_dd)
-            for (uint32_t k = tid; k < rd.nlist; k += NT_MTP)
-                if (did_l[k] == d) atomicMax(&s_fd, (int)k);
+        // d's entry in each list: a short list is a KEPT_CAP list, a long one
+        // the row's sorted keys (found by scan) or its dense row (read by id)
+        const size_t Vz = (size_t)a.vocab;
+        const bool big_t = (rt.flags & RSF_LIST_IN_ROW) != 0u;
+        const bool big_d = has_dd && (rd.flags & RSF_LIST_IN_ROW) != 0u;
+        auto find = [&](int row, const RowState& rs_, bool big, const uint32_t* idl, int* slot) {
+            if (!big) {
+                for (uint32_t k = tid; k < rs_.nlist; k += NT_MTP)
+                    if (idl[k] == d) atomicMax(slot, (int)k);
+            } else if (rs_.sorted) {
+                const uint64_t* kp = a.ckey + (size_t)row * Vz;
+                for (uint32_t k = tid; k < rs_.nlist; k += NT_MTP)
+                    if (pdesc_id(kp[k]) == d) atomicMax(slot, (int)k);
+            }
+        };
+        // the raw p of d (-1 when d is not an entry)
+        auto praw = [&](int row, const RowState& rs_, bool big, const float* pl, int slot) -> float {
+            if (!big) return slot >= 0 ? pl[slot] : -1.0f;
+            if (rs_.sorted) return slot >= 0 ? pdesc_p(a.ckey[(size_t)row * Vz + (uint32_t)slot]) : -1.0f;
+            const float v = d < (uint32_t)a.vocab ? a.dense[(size_t)row * Vz + d] : 0.0f;
+            return v > 0.0f ? v : -1.0f;
+        };
+        find(tr, rt, big_t, tid_l, &s_ft);
+        if (has_dd) find(dr, rd, big_d, did_l, &s_fd);
         __syncthreads();
+        const float rawt = praw(tr, rt, big_t, tp_l, s_ft);
+        const float rawd = has_dd ? praw(dr, rd, big_d, dp_l, s_fd) : -1.0f;
         // normalised entries p / F (TokenDistribution::new, sampling.rs:128-144)
-        const float pt = fmaxf(s_ft >= 0 ? __fdiv_rn(tp_l[s_ft], rt.F) : 0.0f, 0.0f);
+        const float pt = fmaxf(rawt >= 0.0f ? __fdiv_rn(rawt, rt.F) : 0.0f, 0.0f);
         float lnq;
         if (a.mtp_lnq_in) {
             lnq = a.mtp_lnq_in[(size_t)b * D + i];
@@ -4060,7 +4096,7 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         } else if (a.mtp_lnq_full) {
             lnq = a.mtp_lnq_full[(size_t)b * D + i];
         } else {
-            lnq = logprob_of(s_fd >= 0 ? __fdiv_rn(dp_l[s_fd], rd.F) : 0.0f);
+            lnq = logprob_of(rawd >= 0.0f ? __fdiv_rn(rawd, rd.F) : 0.0f);
         }
         float lps = lnq;
         if (has_dd && Td > 0.0f && Tt > 0.0f && fabsf(__fsub_rn(Td, Tt)) > 1e-6f)
@@ -4088,6 +4124,95 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         // draft entry found by binary search, all in parallel; the
         // reference's sequential f32 sums run on one thread over LDS.
         const float ut = mtp_uniform(a, b, tp, stream ? nu : (uint32_t)D);
+        if (big_t || big_d) {
+            // A list too long for the KEPT_CAP lists: the residual over every
+            // id in ascending order, in global memory — P and Q by id in the
+            // rows' dense buffers (a sorted row's list scattered there first;
+            // an index-order row's dense row is its distribution), the terms
+            // and running sums in the target row's ckey2 buffer (free by now),
+            // the reference's sequential sums by the exact block scan.
+            const uint32_t V = (uint32_t)a.vocab;
+            float* Pd = a.dense + (size_t)tr * Vz;
+            float* Qd = has_dd ? a.dense + (size_t)dr * Vz : nullptr;
+            float* W = reinterpret_cast<float*>(a.ckey2 + (size_t)tr * Vz);
+            float* Cs = W + V;
+            auto by_id = [&](int row, const RowState& rs_, bool big, const uint32_t* idl, const float* pl, float* dst) {
+                if (!rs_.sorted) return;  // the dense row holds p; its entries are p > 0
+                for (uint32_t k = tid; k < V; k += NT_MTP) dst[k] = 0.0f;
+                __threadfence_block();
+                __syncthreads();
+                const uint64_t* kp = a.ckey + (size_t)row * Vz;
+                for (uint32_t k = tid; k < rs_.nlist; k += NT_MTP) {
+                    if (big) dst[pdesc_id(kp[k])] = pdesc_p(kp[k]);
+                    else dst[idl[k]] = pl[k];
+                }
+                __threadfence_block();
+                __syncthreads();
+            };
+            by_id(tr, rt, big_t, tid_l, tp_l, Pd);
+            if (has_dd) by_id(dr, rd, big_d, did_l, dp_l, Qd);
+            // residual terms over the target's entries; an id only in Q
+            // carries max(0 - q, 0) = 0 and is no entry of the walk
+            for (uint32_t k = tid; k < V; k += NT_MTP) {
+                const float pr = Pd[k];
+                float w = 0.0f;
+                if (pr > 0.0f) {
+                    const float ptk = __fdiv_rn(pr, rt.F);
+                    float qk = 0.0f;
+                    if (has_dd) qk = Qd[k] > 0.0f ? __fdiv_rn(Qd[k], rd.F) : 0.0f;
+                    else if (k == d) qk = 1.0f;
+                    const float v = fmaxf(__fsub_rn(ptk, qk), 0.0f);
+                    w = (v > 0.0f && isfinite(v)) ? v : 0.0f;
+                }
+                W[k] = w;
+            }
+            __threadfence_block();
+            __syncthreads();
+            const float rsum = block_exact_sums<8>([&](uint32_t k) { return W[k]; }, 0u, V, 0.0f, nullptr, s_sum);
+            // the walk: position k's id and normalised value (-1: no entry)
+            const bool resid = rsum > 0.0f && isfinite(rsum);
+            uint32_t nwalk = V;
+            if (resid) {
+                for (uint32_t k = tid; k < V; k += NT_MTP) W[k] = W[k] > 0.0f ? __fdiv_rn(W[k], rsum) : -1.0f;
+            } else if (rt.sorted) {
+                // empty residual: the target itself, in its kept order (sampling.rs:749)
+                nwalk = rt.nlist;
+                const uint64_t* kp = a.ckey + (size_t)tr * Vz;
+                for (uint32_t k = tid; k < nwalk; k += NT_MTP)
+                    W[k] = __fdiv_rn(big_t ? pdesc_p(kp[k]) : tp_l[k], rt.F);
+            } else {
+                for (uint32_t k = tid; k < V; k += NT_MTP) W[k] = Pd[k] > 0.0f ? __fdiv_rn(Pd[k], rt.F) : -1.0f;
+            }
+            if (tid == 0) {
+                s_cr = NONE;
+                s_mx = 0ull;
+            }
+            __threadfence_block();
+            __syncthreads();
+            const float total = block_exact_sums<8>([&](uint32_t k) { return W[k] < 0.0f ? 0.0f : W[k]; }, 0u, nwalk,
+                                                    0.0f, Cs, s_sum);
+            const float thr = __fmul_rn(ut, total);
+            for (uint32_t k = tid; k < nwalk; k += NT_MTP) {
+                const float q = W[k];
+                if (q < 0.0f) continue;
+                if (Cs[k] >= thr) atomicMin(&s_cr, k);
+                atomicMax(&s_mx, ((uint64_t)__float_as_uint(q) << 32) | (k + 1u));
+            }
+            __syncthreads();
+            if (tid == 0) {
+                const uint32_t cr = s_cr;
+                const uint64_t mx = s_mx;
+                const uint32_t kpos = cr != NONE ? cr : (mx ? (uint32_t)mx - 1u : NONE);
+                uint32_t id = kpos;
+                if (kpos != NONE && !resid && rt.sorted)
+                    id = big_t ? pdesc_id(a.ckey[(size_t)tr * Vz + kpos]) : tid_l[kpos];
+                s_corr = id;
+            }
+            __syncthreads();
+            corr = s_corr;
+            flags |= AXS_MTP_FLAG_RESIDUAL;
+            break;
+        }
         const uint32_t nt = rt.nlist, nd = has_dd ? rd.nlist : 1u;
         // a kept list to ascending id order: each entry's position is the
         // number of smaller ids (the ids of a list are distinct), counted

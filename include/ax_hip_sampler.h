@@ -189,9 +189,10 @@ typedef struct axs_outputs {
  * Uniforms: [batch, depth + 1]; slot i < depth is position i's accept uniform,
  * slot depth the residual/bonus uniform.  NULL = Philox counter
  * (row, step_lo, step_hi, 1), words 0..3 then (row, step_lo, step_hi, 2) ...
- * A sequence one of whose distributions keeps more than 2048 ids is declined
- * (AXS_MTP_FLAG_ERROR, out_count 0): the caller uses the CPU law for it, as
- * the reference's GPU helpers decline with None
+ * Distributions of any size are verified on the device (a kept list of more
+ * than 2048 ids is read from its row's buffers).  A sequence whose row input
+ * is invalid is declined (AXS_MTP_FLAG_ERROR, out_count 0): the caller uses
+ * the CPU law for it, as the reference's GPU helpers decline with None
  * (crates/ax-engine-mlx/src/generate.rs:221-238).
  */
 typedef struct axs_mtp_desc {
