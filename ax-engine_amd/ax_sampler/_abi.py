@@ -71,12 +71,13 @@ EXPORTS = (
     "axs_token_logprob_batch",
     "axs_soft_close_probe",
     "axs_top_logprobs",
+    "axs_lm_head",
     "axs_timing_enable",
     "axs_timing_read",
 )
 
-KERNEL_STREAM, KERNEL_EXACT_MAT, KERNEL_EXACT_ROW, KERNEL_MTP = range(4)
-KERNEL_NAMES = ("k_stream", "k_exact_mat", "k_exact_row", "k_mtp_verify")
+KERNEL_STREAM, KERNEL_EXACT_MAT, KERNEL_EXACT_ROW, KERNEL_MTP, KERNEL_LM_HEAD = range(5)
+KERNEL_NAMES = ("k_stream", "k_exact_mat", "k_exact_row", "k_mtp_verify", "k_lm_head")
 
 
 def build_library(verbose: bool = False) -> str:
@@ -211,6 +212,9 @@ def lib():
             L.axs_top_logprobs.argtypes = [vp, vp, i32, i32, i32, i64, vp, i32, vp, vp, vp]
             L.axs_soft_close_probe.restype = i32
             L.axs_soft_close_probe.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
+            L.axs_lm_head.restype = i32
+            L.axs_lm_head.argtypes = [vp, vp, i64, vp, i64, i32, i32, i32, C.c_float, C.c_float, vp, i64, vp,
+                                      vp]
             L.axs_mtp_verify_ex.restype = i32
             L.axs_mtp_verify_ex.argtypes = [vp, C.POINTER(MtpDesc), C.POINTER(MtpOptions), C.POINTER(MtpOutputs), vp]
             L.axs_mtp_verify.restype = i32

@@ -404,6 +404,30 @@ class HipSampler:
                                            lp.data_ptr(), self._stream(stream)))
         return ids, lp
 
+    def lm_head(self, hidden, weight, scale: float = 1.0, softcap: float = 0.0, want_logits: bool = True,
+                want_argmax: bool = True, stream=None):
+        """The LM-head projection with the greedy decision fused (axs_lm_head):
+        hidden bf16 [B, H], weight bf16 [V, H] on the device.  Returns
+        (logits f32 [B, V] or None, argmax int32 [B] holding uint32 ids or
+        None)."""
+        torch = _torch()
+        if hidden.dtype != torch.bfloat16 or weight.dtype != torch.bfloat16:
+            raise ValueError("hidden and weight must be bfloat16")
+        if hidden.stride(1) != 1:
+            hidden = hidden.contiguous()
+        if weight.stride(1) != 1:
+            weight = weight.contiguous()
+        B, H = hidden.shape
+        V = weight.shape[0]
+        logits = torch.empty((B, V), dtype=torch.float32, device=self.device) if want_logits else None
+        ids = torch.empty(B, dtype=torch.int32, device=self.device) if want_argmax else None
+        _abi.check(self.L.axs_lm_head(self.ctx, hidden.data_ptr(), hidden.stride(0), weight.data_ptr(),
+                                      weight.stride(0), B, H, V, float(scale), float(softcap),
+                                      logits.data_ptr() if logits is not None else None,
+                                      logits.stride(0) if logits is not None else 0,
+                                      ids.data_ptr() if ids is not None else None, self._stream(stream)))
+        return logits, ids
+
     def soft_close_probe(self, logits, think_ids, ranks, stream=None):
         """think_soft_close_in_top_k per row (axs_soft_close_probe): 1 when
         think_ids[r] is within the top ranks[r] raw logits of row r, else 0

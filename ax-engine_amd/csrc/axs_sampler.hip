@@ -41,6 +41,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <cmath>
 #include <cstdlib>
 #include <mutex>
 #include <type_traits>
@@ -49,6 +50,7 @@
 #include <vector>
 
 #include "axs_device.h"
+#include "axs_lm_head.h"
 
 namespace axs {
 
@@ -5325,6 +5327,76 @@ int axs_soft_close_probe(axs_context* ctx, const void* logits, int dtype, int ba
     else
         hipLaunchKernelGGL((k_probe<AXS_DTYPE_F32>), dim3(batch), dim3(NT_PROBE), 0, s, a, think_ids, ranks, out_hit);
     AXS_HIP_CHECK(hipGetLastError());
+    return order_end(ctx, s);
+}
+
+int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, const void* weight,
+                int64_t weight_stride, int batch, int hidden_size, int vocab, float scale, float softcap,
+                float* out_logits, int64_t out_stride, uint32_t* out_argmax, void* stream) {
+    if (!ctx || !hidden || !weight) return fail(AXS_E_INVALID, "ctx, hidden and weight must be non-NULL");
+    if (!out_logits && !out_argmax) return fail(AXS_E_INVALID, "out_logits and out_argmax are both NULL");
+    if (batch < 1 || vocab < 1 || hidden_size < 32 || hidden_size % 32 != 0)
+        return fail(AXS_E_INVALID, "bad shape (hidden_size must be a positive multiple of 32)");
+    if (hidden_stride < hidden_size || weight_stride < hidden_size || hidden_stride % 8 || weight_stride % 8)
+        return fail(AXS_E_INVALID, "hidden_stride and weight_stride must be >= hidden_size and multiples of 8");
+    if (((uintptr_t)hidden | (uintptr_t)weight) & 15)
+        return fail(AXS_E_INVALID, "hidden and weight must be 16-byte aligned");
+    if (out_logits && out_stride < vocab) return fail(AXS_E_INVALID, "out_stride < vocab");
+    if (!std::isfinite(scale) || std::isnan(softcap)) return fail(AXS_E_INVALID, "scale must be finite");
+    if (batch > ctx->max_rows) return fail(AXS_E_CAPACITY, "batch larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DevGuard g(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = order_begin(ctx, s);
+    if (rc) return rc;
+    axs_lmh::LmArgs a{};
+    a.hidden = (const uint16_t*)hidden;
+    a.hs = hidden_stride;
+    a.w = (const uint16_t*)weight;
+    a.ws = weight_stride;
+    a.B = batch;
+    a.H = hidden_size;
+    a.V = vocab;
+    a.scale = scale;
+    a.cap = softcap > 0.0f ? softcap : 0.0f;
+    a.inv_cap = softcap > 0.0f ? 1.0f / softcap : 0.0f;
+    a.out = out_logits;
+    a.os = out_stride;
+    a.keys = out_argmax ? (unsigned long long*)ctx->tmp64 : nullptr;
+    if (a.keys) {
+        hipLaunchKernelGGL(k_fill_u32, dim3((2 * batch + 255) / 256), dim3(256), 0, s, (uint32_t*)a.keys,
+                           (uint32_t)(2 * batch), 0u);
+        AXS_HIP_CHECK(hipGetLastError());
+    }
+    using namespace axs_lmh;
+    timed(ctx, AXS_KERNEL_LM_HEAD, s, [&] {
+        if (batch <= DOT_BMAX) {
+            const dim3 grid((unsigned)((vocab + (NT / 64) * DOT_ROWS - 1) / ((NT / 64) * DOT_ROWS)));
+            if (batch == 1)
+                hipLaunchKernelGGL(k_lm_head_dot<1>, grid, dim3(NT), 0, s, a);
+            else
+                hipLaunchKernelGGL(k_lm_head_dot<2>, grid, dim3(NT), 0, s, a);
+        } else {
+            // up to 32 batch rows: 64 vocabulary rows per workgroup, 512-byte
+            // K chunks; above: 128 rows per workgroup (each hidden fragment
+            // feeds two matrix-core steps), 256-byte chunks
+            const int nb = batch < BMAX ? (batch + 15) / 16 : 4;  // 16-row batch blocks per slice
+            const int rows = nb <= 2 ? 64 : 128;
+            const dim3 grid((unsigned)((vocab + rows - 1) / rows), (unsigned)((batch + BMAX - 1) / BMAX));
+            switch (nb) {
+                case 1: hipLaunchKernelGGL((k_lm_head_mfma<1, 1, 256>), grid, dim3(NT), 0, s, a); break;
+                case 2: hipLaunchKernelGGL((k_lm_head_mfma<2, 1, 256>), grid, dim3(NT), 0, s, a); break;
+                case 3: hipLaunchKernelGGL((k_lm_head_mfma<3, 2, 128>), grid, dim3(NT), 0, s, a); break;
+                default: hipLaunchKernelGGL((k_lm_head_mfma<4, 2, 128>), grid, dim3(NT), 0, s, a); break;
+            }
+        }
+    });
+    AXS_HIP_CHECK(hipGetLastError());
+    if (out_argmax) {
+        hipLaunchKernelGGL(axs_lmh::k_lm_head_ids, dim3((batch + 255) / 256), dim3(256), 0, s, a.keys, batch,
+                           out_argmax);
+        AXS_HIP_CHECK(hipGetLastError());
+    }
     return order_end(ctx, s);
 }
 

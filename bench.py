@@ -54,7 +54,10 @@ WORKLOADS = {
           "top_p 0.95, min_p 0.02, 2048-token histories, Philox draws",
     "C4": "C4: B=128 V=151936 f32, allowed-token bitmask 5-60%, 32 bias entries/row, T 1.0, top_p 0.9",
     "C5": "C5: MTP verify B=32 depth 3 V=151936 bf16, target [B,4,V] + draft [B,3,V], T 0.6, top_p 0.95",
+    "F2": "F2: LM head + greedy argmax (producer fusion) B=64 H=4096 V=151936, bf16 hidden and weight, "
+          "f32 logits written",
 }
+F2_SHAPE = (64, 4096, 151936)  # batch rows, hidden size, vocabulary
 
 
 def log(msg):
@@ -129,6 +132,28 @@ def cpu_baseline_mtp(t, d, tp, dp, dids):
         oracle.mtp_verify_batch(t, d, DTYPE_BF16, B, D1 - 1, V, V, dids, tp, dp, uniforms=us, nthreads=threads)
 
     return cpu_rows_per_s(fn, B), f"all {B} sequences, bf16 target/draft widened on the host"
+
+
+def cpu_baseline_lm_head(torch, hidden, weight):
+    """A CPU statement of the LM-head step (f32 product of bf16 values,
+    bf16 rounding, argmax) over a slice of the weight rows, scaled to the
+    whole vocabulary; torch's CPU matmul on the host's cores."""
+    B, H = hidden.shape
+    V = weight.shape[0]
+    part = 8192
+    h = hidden.float().cpu()
+    w = weight[:part].float().cpu()
+
+    def fn(threads):
+        torch.set_num_threads(threads)
+        y = (h @ w.T).to(torch.bfloat16).float()
+        y.argmax(dim=1)
+
+    res = cpu_rows_per_s(fn, B)
+    scale = part / V  # rows/s over the slice -> over the full vocabulary
+    res = {k: (v[0] * scale, v[1], v[2]) for k, v in res.items()}
+    return res, (f"all {B} batch rows against {part} of the {V} weight rows (f32 matmul of the bf16 values, "
+                 "bf16 rounding, argmax), rate scaled to the full vocabulary")
 
 
 def rotating_sets(base, nbytes, torch):
@@ -207,7 +232,29 @@ def main():
     stream = torch.cuda.current_stream(dev)
     s = HipSampler(0, max_batch=256, max_vocab=262144)
     t0 = time.perf_counter()
-    if cfg == "C5":
+    if cfg == "F2":
+        B, H, V = F2_SHAPE
+        gen = torch.Generator(device=dev).manual_seed(2)
+        weight = (torch.randn(V, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
+        hidden = torch.randn(B, H, device=dev, generator=gen).to(torch.bfloat16)
+        logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+        ids = torch.empty(B, dtype=torch.int32, device=dev)
+        log(f"workload generated in {time.perf_counter() - t0:.1f}s")
+        sptr = s._stream(stream)
+
+        class _Res:
+            token_ids = ids
+
+        def step(i):
+            _abi.check(s.L.axs_lm_head(s.ctx, hidden.data_ptr(), H, weight.data_ptr(), H, B, H, V, 1.0, 0.0,
+                                       logits.data_ptr(), V, ids.data_ptr(), sptr))
+            return _Res
+
+        rows_per_step = B
+        # the weight (1.24 GB, larger than the MALL) is read once per step
+        alg = V * H * 2 + B * H * 2 + B * V * 4 + B * 4
+        unit_rows = "rows/s"
+    elif cfg == "C5":
         from oracle import oracle
 
         t, d, tp, dp = synth.make_c5(5)
@@ -285,11 +332,11 @@ def main():
         dom_us = ms_step * 1e3
         timing_src = "step time (one launch per step, back to back)"
     prof = profile_figures(cfg)
-    if dom_name in ("k_row", "k_stream"):
+    if dom_name in ("k_row", "k_stream", "k_lm_head"):
         dom_alg = alg
     elif dom_name == "k_exact_mat":
         # the second pass re-reads the listed rows (and their mask words)
-        fl = res.flags.cpu().numpy().view(np.uint32) if cfg != "C5" else None
+        fl = res.flags.cpu().numpy().view(np.uint32) if cfg not in ("C5", "F2") else None
         n_ex = int(np.count_nonzero(fl & np.uint32(_abi.FLAG_EXACT_PATH))) if fl is not None else rows_per_step
         dom_alg = int(alg * n_ex / max(rows_per_step, 1))
     else:
@@ -298,7 +345,9 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        if cfg == "C5":
+        if cfg == "F2":
+            cb, sample = cpu_baseline_lm_head(torch, hidden, weight)
+        elif cfg == "C5":
             cb, sample = cpu_baseline_mtp(t, d, tp, dp, dids)
         else:
             cb, sample = cpu_baseline_sample(w)
@@ -325,7 +374,8 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if cfg in ("C1", "C4") else "bf16",
-        "data": "synthetic (seeded, rotating input sets over more than 512 MB)",
+        "data": ("synthetic (seeded; the 1.24 GB weight exceeds the 256 MB MALL)" if cfg == "F2"
+                 else "synthetic (seeded, rotating input sets over more than 512 MB)"),
         "config": {"workload": WORKLOADS[cfg], "global_batch": rows_per_step},
         "roofline": {
             "bound": "hbm",

@@ -386,6 +386,32 @@ int axs_soft_close_probe(axs_context* ctx, const void* logits, int dtype, int ba
                          int64_t row_stride, const uint32_t* think_ids, const uint32_t* ranks,
                          uint32_t* out_hit, void* stream);
 
+/* LM-head projection with the greedy decision in its epilogue (producer
+ * fusion): for every batch row b and vocabulary id v,
+ *   logits[b, v] = softcap(scale * f32(bf16(sum_k hidden[b, k] * weight[v, k])))
+ * the reference's final projection (crates/ax-engine-mlx/src/model/mod.rs:1771-1775:
+ * the bf16 product widened to f32) followed by apply_final_logit_softcap
+ * (crates/ax-engine-mlx/src/model/shared/utils.rs:1826-1845: x * scale, then
+ * tanh(x * (1 / cap)) * cap, in f32; scale 1 and softcap <= 0 turn them
+ * off).  The products accumulate in f32 on the matrix cores and are rounded
+ * to bf16 (nearest even) once, as a bf16 matmul's output is; only the
+ * accumulation order differs from the reference's backend.
+ * hidden [batch, hidden_stride] and weight [vocab, weight_stride] are bf16
+ * device arrays (the final-norm output and the LM-head weight in its
+ * [out, in] layout; quantised weights are not taken).  out_logits
+ * [batch, out_stride] f32 receives the logits when non-NULL; out_argmax
+ * [batch] receives each row's argmax under argmax_f32
+ * (crates/ax-engine-mlx/src/sampling.rs:954-970: first maximum, NaN skipped,
+ * an all-NaN row gives 0) when non-NULL, formed in the same kernel, so a
+ * greedy row's logits need never be written.  Rows to be sampled go on to
+ * axs_sample_batch over out_logits.  Requires hidden_size % 32 == 0, both
+ * input strides multiples of 8 elements and 16-byte aligned inputs;
+ * batch <= the context's max_batch (argmax keys live in its workspace).
+ * The weight is read from HBM once per 64 batch rows. */
+int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, const void* weight,
+                int64_t weight_stride, int batch, int hidden_size, int vocab, float scale, float softcap,
+                float* out_logits, int64_t out_stride, uint32_t* out_argmax, void* stream);
+
 /* MTP speculative verify (see axs_mtp_desc). */
 /* MTP verify with options: per sequence, mtp_accept_count
  * (crates/ax-engine-mlx/src/runner/mod.rs:12333-12462) over the draft ids,
@@ -415,7 +441,8 @@ int axs_mtp_verify(axs_context* ctx, const axs_mtp_desc* desc,
 #define AXS_KERNEL_EXACT_MAT 1  /* exact path: second pass            */
 #define AXS_KERNEL_EXACT_ROW 2  /* exact path: sort + exact sums      */
 #define AXS_KERNEL_MTP       3  /* MTP accept / residual / bonus      */
-#define AXS_KERNEL_COUNT     4
+#define AXS_KERNEL_LM_HEAD   4  /* LM-head projection + argmax        */
+#define AXS_KERNEL_COUNT     5
 int axs_timing_enable(axs_context* ctx, int enable);
 /* Waits for the recorded events of one kernel class and returns their summed
  * duration in milliseconds and the number of launches since enabling. */

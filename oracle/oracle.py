@@ -293,6 +293,50 @@ def top_logprobs(logits, temperature: float, n: int):
     return ids[:n], lp[:n]
 
 
+MTP_DRAFT_SAMPLED, MTP_DRAFT_STOCHASTIC = 0, 1
+
+
+def mtp_draft(logits, temperature: float, mode: int, u: float):
+    """The draft side of one MTP depth on one draft row: (token, ln q, explain
+    record of the draw or None).
+
+    mode MTP_DRAFT_SAMPLED, mtp_draft_tokens_sampled
+    (crates/ax-engine-mlx/src/mtp.rs:1454-1552): the token is the argmax
+    (lazy_argmax_logits, mtp.rs:192-196) and ln q its full-softmax log-prob at
+    the draft temperature (gpu_draft_log_prob_lazy, mtp.rs:203-220).
+
+    mode MTP_DRAFT_STOCHASTIC, mtp_draft_tokens_stochastic (mtp.rs:1554-1640):
+    for T > 0 a categorical draw from softmax(logits / T) (lazy_random_sample,
+    mtp.rs:228-233), ln q at T; for T <= 0 the argmax, ln q at T = 1
+    (mtp.rs:1614-1623).  The reference draws with MLX's own RNG (not
+    reproducible); the draw here is sample_categorical_into with no filters
+    (crates/ax-engine-mlx/src/sampling.rs:204-271, the index-order law) on the
+    supplied uniform u.  ln q is full_vocab_token_logprob
+    (crates/ax-engine-mlx/src/sampling.rs:761-787), the CPU statement of
+    gpu_draft_log_prob_lazy's value."""
+    a = _f32(logits)
+    T = float(np.float32(temperature))
+    ex = None
+    if mode == MTP_DRAFT_SAMPLED or T <= 0.0:
+        tok = argmax_f32(a)
+    else:
+        p = np.zeros(1, dtype=_params_dtype())
+        p["temperature"] = T
+        p["top_p"] = 1.0
+        p["repetition_penalty"] = 1.0
+        p["repetition_context_size"] = NONE_U32
+        p["ngram_window"] = 128
+        tok, ex, _ = sample_row(a, p, u=u)
+    lp_t = T if (mode == MTP_DRAFT_SAMPLED or T > 0.0) else 1.0
+    return tok, full_vocab_token_logprob(a, tok, lp_t), ex
+
+
+def _params_dtype():
+    from ax_sampler.params import PARAMS_DTYPE
+
+    return PARAMS_DTYPE
+
+
 def soft_close_in_top_k(logits, target: int, rank: int) -> bool:
     a = _f32(logits)
     if a.size == 0:

@@ -571,3 +571,48 @@ def test_top_logprobs_edge_cases(oracle):
     ids, lp = oracle.top_logprobs(x, 1.0, 5)  # ties to the lower id; p(NaN) = p(-inf) = 0
     assert ids.tolist() == [1, 2, 0, 3, 4]
     assert lp[3] == -30.0 and lp[4] == -30.0
+
+
+def _log_softmax64(x, T):
+    z = x.astype(np.float64) / T
+    z = z - z.max()
+    return z - np.log(np.exp(z).sum())
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_mtp_draft_sampled_mode_is_argmax_with_full_softmax_logprob(oracle, seed):
+    """mtp_draft_tokens_sampled: the argmax and ln softmax(l / T) of it (float64
+    closed form, within 1e-5)."""
+    rng = np.random.default_rng([seed, 31])
+    for trial in range(5):
+        V = int(rng.integers(2, 3000))
+        x = (rng.standard_normal(V) * 3.0).astype(np.float32)
+        T = float(rng.choice([0.6, 1.0, 1.3]))
+        tok, lnq, ex = oracle.mtp_draft(x, T, oracle.MTP_DRAFT_SAMPLED, 0.5)
+        assert ex is None and tok == int(np.argmax(x))
+        assert abs(lnq - max(_log_softmax64(x, T)[tok], -30.0)) < 1e-5
+
+
+@pytest.mark.parametrize("seed", range(3))
+def test_mtp_draft_stochastic_mode_inverts_the_softmax_cdf(oracle, seed):
+    """mtp_draft_tokens_stochastic at T > 0: the token whose float64 CDF
+    interval holds u (draws within 1e-5 of an interval end skipped), with
+    ln softmax(l / T) of it; at T <= 0 the argmax with ln q at T = 1."""
+    rng = np.random.default_rng([seed, 37])
+    V = 500
+    x = (rng.standard_normal(V) * 2.0).astype(np.float32)
+    T = 0.8
+    p = np.exp(_log_softmax64(x, T))
+    cdf = np.cumsum(p)
+    checked = 0
+    for u in np.linspace(0.001, 0.999, 200).astype(np.float32):
+        tok, lnq, ex = oracle.mtp_draft(x, T, oracle.MTP_DRAFT_STOCHASTIC, float(u))
+        lo = cdf[tok] - p[tok]
+        if min(abs(float(u) - lo), abs(float(u) - cdf[tok])) > 1e-5:
+            assert lo <= float(u) < cdf[tok], (u, tok)
+            checked += 1
+        assert abs(lnq - max(_log_softmax64(x, T)[tok], -30.0)) < 1e-5
+    assert checked > 190
+    tok, lnq, _ = oracle.mtp_draft(x, 0.0, oracle.MTP_DRAFT_STOCHASTIC, 0.3)
+    assert tok == int(np.argmax(x))
+    assert abs(lnq - _log_softmax64(x, 1.0)[tok]) < 1e-5
