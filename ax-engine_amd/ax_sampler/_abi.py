@@ -44,6 +44,7 @@ MTP_SRC_DEFAULT, MTP_SRC_MTP, MTP_SRC_GEMMA, MTP_SRC_NGRAM, MTP_SRC_HYBRID = ran
 MTP_MODEL_GREEDY, MTP_MODEL_REJECTION = 0, 1
 MTP_NGRAM_CONFIDENCE, MTP_NGRAM_DELTA, MTP_NGRAM_GREEDY = 0, 1, 2
 MTP_LNQ_DISTRIBUTION, MTP_LNQ_FULL_SOFTMAX = 0, 1
+MTP_DRAFT_SAMPLED, MTP_DRAFT_STOCHASTIC = 0, 1
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -72,6 +73,7 @@ EXPORTS = (
     "axs_soft_close_probe",
     "axs_top_logprobs",
     "axs_lm_head",
+    "axs_mtp_draft",
     "axs_timing_enable",
     "axs_timing_read",
 )
@@ -212,6 +214,8 @@ def lib():
             L.axs_top_logprobs.argtypes = [vp, vp, i32, i32, i32, i64, vp, i32, vp, vp, vp]
             L.axs_soft_close_probe.restype = i32
             L.axs_soft_close_probe.argtypes = [vp, vp, i32, i32, i32, i64, vp, vp, vp, vp]
+            L.axs_mtp_draft.restype = i32
+            L.axs_mtp_draft.argtypes = [vp, vp, i32, i32, i32, i64, vp, i32, vp, vp, vp, vp]
             L.axs_lm_head.restype = i32
             L.axs_lm_head.argtypes = [vp, vp, i64, vp, i64, i32, i32, i32, C.c_float, C.c_float, vp, i64, vp,
                                       vp]

@@ -404,6 +404,29 @@ class HipSampler:
                                            lp.data_ptr(), self._stream(stream)))
         return ids, lp
 
+    def mtp_draft(self, logits, params, mode: int, uniforms=None, stream=None):
+        """One MTP draft depth (axs_mtp_draft): the draft token of every row
+        (argmax, or a categorical draw at the row's temperature) and its
+        full-softmax log-prob.  params: PARAMS_DTYPE [B] (numpy or a device
+        uint8 tensor); returns (ids int32 [B] holding uint32 ids, lnq f32 [B])
+        on the device."""
+        torch = _torch()
+        if logits.stride(1) != 1:
+            logits = logits.contiguous()
+        B, V = logits.shape
+        pd = params if isinstance(params, torch.Tensor) else torch.from_numpy(
+            np.ascontiguousarray(params).view(np.uint8)).to(self.device)
+        ud = None
+        if uniforms is not None:
+            ud = uniforms if isinstance(uniforms, torch.Tensor) else torch.from_numpy(
+                np.ascontiguousarray(np.asarray(uniforms, dtype=np.float32))).to(self.device)
+        ids = torch.empty(B, dtype=torch.int32, device=self.device)
+        lnq = torch.empty(B, dtype=torch.float32, device=self.device)
+        _abi.check(self.L.axs_mtp_draft(self.ctx, logits.data_ptr(), _dtype_code(logits), B, V, logits.stride(0),
+                                        pd.data_ptr(), int(mode), ud.data_ptr() if ud is not None else None,
+                                        ids.data_ptr(), lnq.data_ptr(), self._stream(stream)))
+        return ids, lnq
+
     def lm_head(self, hidden, weight, scale: float = 1.0, softcap: float = 0.0, want_logits: bool = True,
                 want_argmax: bool = True, stream=None):
         """The LM-head projection with the greedy decision fused (axs_lm_head):

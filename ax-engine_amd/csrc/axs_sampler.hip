@@ -4550,6 +4550,7 @@ struct axs_context {
     float* mtp_lnq;     // full-softmax draft log-probs [rows]
     uint32_t* lp_tok;   // token echo of the draft log-prob pass [rows]
     float* lp_temps;    // draft temperatures per draft row [rows]
+    axs_sampling_params* draft_par;  // axs_mtp_draft: the draft law's params [rows]
     bool timing;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> ev[AXS_KERNEL_COUNT];
     // Calls are serialised: the lock covers each call's enqueue, and a call
@@ -4602,7 +4603,8 @@ void free_ctx(axs_context* c) {
     if (c->own_stream) (void)hipStreamDestroy(c->own_stream);
     void* ptrs[] = {c->cstat, c->pool, c->rstate,  c->exact_rows, c->exact_count,
                     c->row_done, c->dense, c->ckey, c->ckey2, c->tmp64, c->sbuf, c->bend,
-                    c->kept_id, c->kept_p, c->mtp_tok, c->mtp_amax, c->mtp_lnq, c->lp_tok, c->lp_temps};
+                    c->kept_id, c->kept_p, c->mtp_tok, c->mtp_amax, c->mtp_lnq, c->lp_tok, c->lp_temps,
+                    c->draft_par};
     for (void* q : ptrs)
         if (q) (void)hipFree(q);
     delete c;
@@ -4964,7 +4966,7 @@ int axs_context_create(int device, int max_batch, int max_vocab, axs_context** o
         (rc = dalloc(&c->sbuf, R * Vv)) || (rc = dalloc(&c->bend, R * BEND_STRIDE)) ||
         (rc = dalloc(&c->kept_id, R * KEPT_CAP)) || (rc = dalloc(&c->kept_p, R * KEPT_CAP)) ||
         (rc = dalloc(&c->mtp_tok, R)) || (rc = dalloc(&c->mtp_amax, R)) || (rc = dalloc(&c->mtp_lnq, R)) ||
-        (rc = dalloc(&c->lp_tok, R)) || (rc = dalloc(&c->lp_temps, R))) {
+        (rc = dalloc(&c->lp_tok, R)) || (rc = dalloc(&c->lp_temps, R)) || (rc = dalloc(&c->draft_par, R))) {
         free_ctx(c);
         return rc;
     }
@@ -5397,6 +5399,88 @@ int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, con
                            out_argmax);
         AXS_HIP_CHECK(hipGetLastError());
     }
+    return order_end(ctx, s);
+}
+
+}  // extern "C"
+
+namespace {
+
+// The draft law of one MTP depth per row (no processors, no filters): the
+// sampled mode's argmax is the greedy law (T = 0), the stochastic mode's
+// draw is sample_categorical_into at T with top_p 1 and top_k 0; lp_temps
+// gets the temperature of the full-softmax log-prob.
+__global__ void k_draft_prep(const axs_sampling_params* in, int n, int mode, axs_sampling_params* out,
+                             float* lp_temps) {
+    const int r = blockIdx.x * blockDim.x + threadIdx.x;
+    if (r >= n) return;
+    const float T = in[r].temperature;
+    axs_sampling_params p{};
+    p.temperature = mode == AXS_MTP_DRAFT_SAMPLED ? 0.0f : T;
+    p.top_p = 1.0f;
+    p.top_k = 0;
+    p.min_p = 0.0f;
+    p.has_min_p = 0;
+    p.repetition_penalty = 1.0f;
+    p.repetition_context_size = AXS_NONE_U32;
+    p.no_repeat_ngram_size = 0;
+    p.ngram_window = 128;
+    p.presence_penalty = 0.0f;
+    p.frequency_penalty = 0.0f;
+    p.seed = in[r].seed;
+    p.step = in[r].step;
+    out[r] = p;
+    lp_temps[r] = (mode == AXS_MTP_DRAFT_SAMPLED || T > 0.0f) ? T : 1.0f;
+}
+
+}  // namespace
+
+extern "C" {
+
+int axs_mtp_draft(axs_context* ctx, const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                  const axs_sampling_params* params, int mode, const float* uniforms, uint32_t* out_ids,
+                  float* out_lnq, void* stream) {
+    if (!ctx || !logits || !params || !out_ids || !out_lnq)
+        return fail(AXS_E_INVALID, "ctx, logits, params, out_ids and out_lnq must be non-NULL");
+    if (dtype != AXS_DTYPE_F32 && dtype != AXS_DTYPE_BF16) return fail(AXS_E_INVALID, "bad dtype");
+    if (mode != AXS_MTP_DRAFT_SAMPLED && mode != AXS_MTP_DRAFT_STOCHASTIC) return fail(AXS_E_INVALID, "bad mode");
+    if (batch < 1 || vocab < 1 || row_stride < vocab) return fail(AXS_E_INVALID, "bad shape");
+    if (batch > ctx->max_rows || vocab > ctx->max_vocab)
+        return fail(AXS_E_CAPACITY, "batch or vocab larger than the context");
+    std::lock_guard<std::mutex> lk(ctx->mu);
+    DevGuard g(ctx->device);
+    hipStream_t s = (hipStream_t)stream;
+    int rc = order_begin(ctx, s);
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_draft_prep, dim3((unsigned)((batch + 255) / 256)), dim3(256), 0, s, params, batch, mode,
+                       ctx->draft_par, ctx->lp_temps);
+    AXS_HIP_CHECK(hipGetLastError());
+    // the draw (or argmax) of every draft row
+    KArgs a{};
+    a.logits = logits;
+    a.dtype = dtype;
+    a.nrows = batch;
+    a.vocab = vocab;
+    a.stride = row_stride;
+    a.params = ctx->draft_par;
+    a.exact_lp = 1;
+    a.uniforms = uniforms;
+    a.out_ids = out_ids;
+    Plan pl = make_plan(dtype, batch, vocab, logits, row_stride, nullptr);
+    if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
+    // ln softmax(l / T)[token] of the drawn tokens, axs_token_logprob_batch's pass
+    KArgs l{};
+    l.logits = logits;
+    l.dtype = dtype;
+    l.nrows = batch;
+    l.vocab = vocab;
+    l.stride = row_stride;
+    l.params = nullptr;
+    l.lp_tokens = out_ids;
+    l.lp_temps = ctx->lp_temps;
+    l.out_ids = ctx->lp_tok;  // the tokens echoed: scratch
+    l.out_lp = out_lnq;
+    if ((rc = run_pipeline(ctx, l, pl, s))) return rc;
     return order_end(ctx, s);
 }
 

@@ -386,6 +386,31 @@ int axs_soft_close_probe(axs_context* ctx, const void* logits, int dtype, int ba
                          int64_t row_stride, const uint32_t* think_ids, const uint32_t* ranks,
                          uint32_t* out_hit, void* stream);
 
+/* MTP draft side, one depth over batch draft rows [batch, row_stride]:
+ * per row the draft token and its full-softmax log-prob ln q, which
+ * axs_mtp_verify_ex consumes as pending_log_probs.
+ *   AXS_MTP_DRAFT_SAMPLED (mtp_draft_tokens_sampled,
+ *     crates/ax-engine-mlx/src/mtp.rs:1454-1552): the argmax
+ *     (lazy_argmax_logits, mtp.rs:192-196), ln q at the row's temperature;
+ *   AXS_MTP_DRAFT_STOCHASTIC (mtp_draft_tokens_stochastic, mtp.rs:1554-1640):
+ *     T > 0 a categorical draw from softmax(l / T) (lazy_random_sample,
+ *     mtp.rs:228-233), ln q at T; T <= 0 the argmax, ln q at T = 1.
+ * ln q = full_vocab_token_logprob(row, token, T)
+ * (crates/ax-engine-mlx/src/sampling.rs:761-787), the CPU statement of
+ * gpu_draft_log_prob_lazy (mtp.rs:203-220), as axs_token_logprob_batch
+ * computes it.  The reference draws with MLX's own generator (its comment:
+ * not reproducible); here the draw is sample_categorical_into with no
+ * filters (sampling.rs:204-271) on uniforms[r] (device [batch], in [0, 1])
+ * or, when uniforms is NULL, Philox(params[r].seed, r, params[r].step).
+ * params [batch] (device): only temperature, seed and step are read; the
+ * draft law applies no processors or filters.  out_ids and out_lnq [batch]:
+ * device arrays. */
+#define AXS_MTP_DRAFT_SAMPLED    0
+#define AXS_MTP_DRAFT_STOCHASTIC 1
+int axs_mtp_draft(axs_context* ctx, const void* logits, int dtype, int batch, int vocab, int64_t row_stride,
+                  const axs_sampling_params* params, int mode, const float* uniforms, uint32_t* out_ids,
+                  float* out_lnq, void* stream);
+
 /* LM-head projection with the greedy decision in its epilogue (producer
  * fusion): for every batch row b and vocabulary id v,
  *   logits[b, v] = softcap(scale * f32(bf16(sum_k hidden[b, k] * weight[v, k])))
