@@ -16,6 +16,7 @@ CSRC = os.path.join(os.path.dirname(PKG_DIR), "csrc")
 INCLUDE = os.path.join(ROOT, "include")
 LIB_PATH = os.path.join(PKG_DIR, "libax_hip_sampler.so")
 
+ABI_VERSION = 2
 AXS_OK = 0
 AXS_DTYPE_F32 = 0
 AXS_DTYPE_BF16 = 1
@@ -45,6 +46,7 @@ MTP_MODEL_GREEDY, MTP_MODEL_REJECTION = 0, 1
 MTP_NGRAM_CONFIDENCE, MTP_NGRAM_DELTA, MTP_NGRAM_GREEDY = 0, 1, 2
 MTP_LNQ_DISTRIBUTION, MTP_LNQ_FULL_SOFTMAX = 0, 1
 MTP_DRAFT_SAMPLED, MTP_DRAFT_STOCHASTIC = 0, 1
+MTP_TARGET_DISTRIBUTION, MTP_TARGET_FILTERED = 0, 1
 
 HIPCC_FLAGS = [
     "--offload-arch=gfx950",
@@ -155,6 +157,8 @@ class MtpOptions(C.Structure):
         ("ngram_mode", C.c_int32),
         ("lnq_mode", C.c_int32),
         ("delta_correction", C.c_int32),
+        ("target_law", C.c_int32),
+        ("target_topk", C.c_uint32),
     ]
 
 
@@ -227,7 +231,7 @@ def lib():
             L.axs_timing_enable.argtypes = [vp, i32]
             L.axs_timing_read.restype = i32
             L.axs_timing_read.argtypes = [vp, i32, C.POINTER(C.c_double), C.POINTER(C.c_int)]
-            if L.axs_abi_version() != 1:
+            if L.axs_abi_version() != ABI_VERSION:
                 raise SamplerError("ABI version mismatch")
             _lib = L
     return _lib

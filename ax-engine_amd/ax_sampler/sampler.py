@@ -475,7 +475,8 @@ class HipSampler:
         """target [B, D+1, V], draft [B, D, V] on device; draft_ids [B, D].
         ``options`` (dict) selects ``axs_mtp_verify_ex``: ``sources`` /
         ``pending_log_probs`` / ``predicted`` ([B, D] arrays or None),
-        ``model_mode``, ``ngram_mode``, ``lnq_mode``, ``delta_correction``;
+        ``model_mode``, ``ngram_mode``, ``lnq_mode``, ``delta_correction``,
+        ``target_law``, ``target_topk``;
         its uniforms are taken in the reference's stream order."""
         torch = _torch()
         B, D1, V = target.shape
@@ -526,6 +527,8 @@ class HipSampler:
         op.ngram_mode = int(options.get("ngram_mode", _abi.MTP_NGRAM_CONFIDENCE))
         op.lnq_mode = int(options.get("lnq_mode", _abi.MTP_LNQ_DISTRIBUTION))
         op.delta_correction = int(bool(options.get("delta_correction", False)))
+        op.target_law = int(options.get("target_law", _abi.MTP_TARGET_DISTRIBUTION))
+        op.target_topk = int(options.get("target_topk", 0))
         _abi.check(self.L.axs_mtp_verify_ex(self.ctx, C.byref(d), C.byref(op), C.byref(o), self._stream(stream)))
         return MtpResult(out_ids, out_n, acc, fl, tuple(keep))
 

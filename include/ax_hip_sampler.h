@@ -36,7 +36,7 @@
 extern "C" {
 #endif
 
-#define AXS_ABI_VERSION 1
+#define AXS_ABI_VERSION 2
 
 /* status codes */
 #define AXS_OK            0
@@ -245,6 +245,18 @@ typedef struct axs_mtp_outputs {
 #define AXS_MTP_NGRAM_GREEDY     2
 #define AXS_MTP_LNQ_DISTRIBUTION 0  /* ln q = ln Q_i(d), Q_i = token_distribution
                                        of draft row i (the filtered law)      */
+#define AXS_MTP_TARGET_DISTRIBUTION 0  /* p(d) = P_i(d), P_i = token_distribution
+                                          of target row i (the sampler's law) */
+#define AXS_MTP_TARGET_FILTERED 1  /* p(d) as the runner forms it for the
+                                      acceptance test: compute_mtp_target_probs
+                                      + extract_cpu_into +
+                                      filtered_target_token_probability
+                                      (crates/ax-engine-mlx/src/runner/mod.rs:
+                                      11836-12159): the softmax of target row i
+                                      (full_vocab_token_logprob's terms and
+                                      sum), its top_k (or target_topk) largest,
+                                      min_p, then top_p cut on the running sum,
+                                      renormalised; the residual still uses P_i */
 #define AXS_MTP_LNQ_FULL_SOFTMAX 1  /* ln q = ln softmax(draft row i / T_d)[d],
                                        the full-vocabulary law of
                                        gpu_draft_log_prob_lazy
@@ -272,6 +284,11 @@ typedef struct axs_mtp_options {
                                            correction, runner/mod.rs:12161-12184);
                                            zero: no correction, the tail is the
                                            target row's own draw                 */
+    int32_t target_law;                 /* AXS_MTP_TARGET_*: the target probability
+                                           of the acceptance test                 */
+    uint32_t target_topk;               /* AXS_MTP_TARGET_FILTERED only: the
+                                           runner's mtp_target_softmax_topk,
+                                           0 = none                              */
 } axs_mtp_options;
 
 typedef struct axs_context axs_context;

@@ -868,6 +868,105 @@ void axo_top_logprobs(const float* logits, uint32_t V, float temperature, uint32
     free(e);
 }
 
+/* The target probability of one draft token under the production MTP law:
+ * compute_mtp_target_probs (runner/mod.rs:12025-12159) followed by
+ * LazyTargetProbs::extract_cpu_into (runner/mod.rs:11836-11937) and
+ * filtered_target_token_probability (runner/mod.rs:11943-12001).  Returns NaN
+ * when the reference computes none (T <= 0: greedy comparisons).
+ *
+ * The row's softmax is full_vocab_token_logprob's statement of it
+ * (sampling.rs:761-787): q_j = exp((l_j - max) / T) with non-finite q as 0,
+ * S their f32 sum in index order, p_j = q_j / S (MLX's softmax reduction
+ * order is not reproducible; this is the reference's own CPU statement).
+ * Then, as compute_mtp_target_probs chooses:
+ *   topk_opt > 0 (mtp_target_softmax_topk): the topk_opt largest p, top_p and
+ *     min_p of the target (LazyTargetProbs::TopK);
+ *   else target top_k > 0 or top_p < 1 (the draft filter is the target's
+ *     own, runner/mod.rs:8643-8646): the top_k (or V) largest p, top_p,
+ *     min_p (TopK);
+ *   else min_p in use: every p, min_p (FullRows ->
+ *     filtered_target_token_probability(row, t, min_p, 1.0, 0));
+ *   else p_t itself (Full).
+ * The filtered cases keep p > 0, then p >= min_p * max p, order by
+ * (p desc, id asc), cut where the f32 running sum first reaches top_p
+ * (0 < top_p < 1; at least one entry) and return p_t over the kept set's
+ * f32 sum in that order, 0 for a token outside it.  The top-k set is taken
+ * in the same order (MLX's argpartition leaves ties at the k-th value in an
+ * unspecified order; here the lower id wins). */
+static int prodp_cmp(const void* a, const void* b) {
+    const topn_ent* x = (const topn_ent*)a;
+    const topn_ent* y = (const topn_ent*)b;
+    if (x->p != y->p) return x->p > y->p ? -1 : 1;
+    return x->id < y->id ? -1 : (x->id > y->id ? 1 : 0);
+}
+
+float axo_mtp_target_prob(const float* logits, uint32_t V, float temperature, float top_p, uint32_t top_k,
+                          int has_min_p, float min_p, uint32_t topk_opt, uint32_t token) {
+    if (!(temperature > 0.0f)) return NAN;
+    if (V == 0) return 0.0f;
+    const float inv = 1.0f / temperature;
+    float m = -INFINITY;
+    for (uint32_t i = 0; i < V; ++i) m = fmaxf(m, logits[i]);
+    float* q = (float*)malloc(sizeof(float) * V);
+    float S = 0.0f;
+    for (uint32_t i = 0; i < V; ++i) {
+        const float e = expf((logits[i] - m) * inv);
+        q[i] = isfinite(e) ? e : 0.0f;
+        S += q[i];
+    }
+    float out = 0.0f;
+    const int uses_min_p = has_min_p && isfinite(min_p) && min_p > 0.0f;
+    if (!(S > 0.0f) || !isfinite(S)) {
+        free(q);
+        return 0.0f;
+    }
+    if (topk_opt == 0 && top_k == 0 && !(top_p < 1.0f) && !uses_min_p) {
+        out = token < V ? q[token] / S : 0.0f;  /* Full: the softmax value itself */
+        free(q);
+        return out;
+    }
+    uint32_t K = V;
+    float tp = top_p;
+    if (topk_opt > 0) K = topk_opt < V ? topk_opt : V;
+    else if (top_k > 0 || top_p < 1.0f) K = (top_k > 0 && top_k < V) ? top_k : V;
+    else tp = 1.0f;  /* FullRows: min_p only */
+    topn_ent* c = (topn_ent*)malloc(sizeof(topn_ent) * V);
+    uint32_t n = 0;
+    for (uint32_t i = 0; i < V; ++i) {
+        const float p = q[i] / S;
+        if (p > 0.0f && isfinite(p)) { c[n].p = p; c[n].id = i; ++n; }
+    }
+    qsort(c, n, sizeof(topn_ent), prodp_cmp);
+    if (n > K) n = K;  /* the top-k set */
+    if (uses_min_p && n > 0) {
+        const float cutoff = min_p * c[0].p;  /* c[0].p: the largest */
+        uint32_t w = 0;
+        for (uint32_t k = 0; k < n; ++k)
+            if (c[k].p >= cutoff) c[w++] = c[k];
+        n = w;
+    }
+    if (isfinite(tp) && tp > 0.0f && tp < 1.0f) {
+        float cum = 0.0f;
+        uint32_t keep = 0;
+        for (uint32_t k = 0; k < n; ++k) {
+            cum += c[k].p;
+            ++keep;
+            if (cum >= tp) break;
+        }
+        n = keep > 0 ? keep : (n > 0 ? 1 : 0);
+    }
+    float sum = 0.0f;
+    for (uint32_t k = 0; k < n; ++k) sum += c[k].p;
+    for (uint32_t k = 0; k < n; ++k)
+        if (c[k].id == token) {
+            out = fmaxf(c[k].p / fmaxf(sum, 1e-37f), 0.0f);
+            break;
+        }
+    free(c);
+    free(q);
+    return out;
+}
+
 /* think_soft_close_in_top_k (crates/ax-engine-mlx/src/ngram_accel.rs:1609-1640):
  * the reference's single pass, kept literally: the first `rank` logits taken
  * as they come and stably sorted descending by total order (f32::total_cmp);

@@ -98,6 +98,8 @@ def lib():
         L.axo_full_vocab_token_logprob.argtypes = [vp, u32, u32, f32]
         L.axo_top_logprobs.restype = None
         L.axo_top_logprobs.argtypes = [vp, u32, f32, u32, vp, vp]
+        L.axo_mtp_target_prob.restype = f32
+        L.axo_mtp_target_prob.argtypes = [vp, u32, f32, f32, u32, i32, f32, u32, u32]
         L.axo_soft_close_in_top_k.restype = C.c_int
         L.axo_soft_close_in_top_k.argtypes = [vp, u32, u32, u32]
         L.axo_mtp_accept_count.restype = u32
@@ -291,6 +293,18 @@ def top_logprobs(logits, temperature: float, n: int):
     lp = np.zeros(max(n, 1), np.float32)
     lib().axo_top_logprobs(a.ctypes.data, a.size, temperature, n, ids.ctypes.data, lp.ctypes.data)
     return ids[:n], lp[:n]
+
+
+def mtp_target_prob(logits, token: int, temperature: float, top_p: float = 1.0, top_k: int = 0,
+                    min_p: Optional[float] = None, topk_opt: int = 0) -> float:
+    """The production law's target probability of a draft token
+    (compute_mtp_target_probs + extract_cpu_into +
+    filtered_target_token_probability, crates/ax-engine-mlx/src/runner/mod.rs:
+    11836-12159; see axo_mtp_target_prob).  NaN when T <= 0."""
+    a = _f32(logits)
+    return float(lib().axo_mtp_target_prob(a.ctypes.data, a.size, temperature, top_p, top_k,
+                                           0 if min_p is None else 1, 0.0 if min_p is None else min_p,
+                                           topk_opt, token))
 
 
 MTP_DRAFT_SAMPLED, MTP_DRAFT_STOCHASTIC = 0, 1

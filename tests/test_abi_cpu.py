@@ -41,7 +41,7 @@ def test_library_loads_without_touching_the_gpu():
 
     L = ctypes.CDLL(_abi.LIB_PATH)
     L.axs_abi_version.restype = ctypes.c_int
-    assert L.axs_abi_version() == 1
+    assert L.axs_abi_version() == 2
     L.axs_last_error.restype = ctypes.c_char_p
     assert L.axs_last_error() == b""
 
@@ -55,7 +55,7 @@ def test_struct_layouts_match_the_header():
     assert ctypes.sizeof(_abi.Outputs) == 48
     assert ctypes.sizeof(_abi.MtpDesc) == 72
     assert ctypes.sizeof(_abi.MtpOutputs) == 32
-    assert ctypes.sizeof(_abi.MtpOptions) == 40
+    assert ctypes.sizeof(_abi.MtpOptions) == 48
 
 
 def test_c_struct_sizes_from_the_compiler(tmp_path):
@@ -68,7 +68,7 @@ def test_c_struct_sizes_from_the_compiler(tmp_path):
     exe = tmp_path / "s"
     subprocess.run(["gcc", "-I", os.path.join(ROOT, "include"), str(src), "-o", str(exe)], check=True)
     sizes = subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()
-    assert sizes == ["64", "120", "48", "72", "32", "40"]
+    assert sizes == ["64", "120", "48", "72", "32", "48"]
 
 
 def test_error_handler_and_last_error_without_a_gpu():

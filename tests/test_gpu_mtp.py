@@ -21,7 +21,7 @@ import numpy as np
 import pytest
 
 from ax_sampler import _abi
-from ax_sampler.synth import DTYPE_BF16, DTYPE_F32, f32_to_bf16_bits, make_c5
+from ax_sampler.synth import DTYPE_BF16, DTYPE_F32, bf16_bits_to_f32, f32_to_bf16_bits, make_c5
 
 from gpu_common import boundary_allowance, log
 
@@ -242,7 +242,13 @@ def _mtp_expect(oracle, tf, df, dids, tp, dp, us, opts, D):
         tests.append((not greedy) and math.isfinite(v) and Tt > 0)
     pred = (list(map(int, opts["predicted"])) if opts.get("predicted") is not None
             else [oracle.argmax_f32(tf[i]) for i in range(D)])
-    tprobs = [max(oracle.distribution_prob(P[i][0], P[i][1], int(dids[i])), 0.0) for i in range(D)] if Tt > 0 else None
+    if Tt > 0 and opts.get("target_law") == _abi.MTP_TARGET_FILTERED:
+        mp = float(tp["min_p"][0]) if int(tp["has_min_p"][0]) else None
+        tprobs = [oracle.mtp_target_prob(tf[i], int(dids[i]), Tt, float(tp["top_p"][0]), int(tp["top_k"][0]), mp,
+                                         int(opts.get("target_topk", 0))) for i in range(D)]
+    else:
+        tprobs = [max(oracle.distribution_prob(P[i][0], P[i][1], int(dids[i])), 0.0) for i in range(D)] \
+            if Tt > 0 else None
     ac, allacc, corr = oracle.mtp_accept_count(
         list(map(int, dids)), lnq, [Q[i] for i in range(D) if src[i] != _abi.MTP_SRC_NGRAM], src, tprobs, P,
         pred, None, Td, Tt, opts.get("model_mode", 1), opts.get("ngram_mode", 0), uniforms=us)
@@ -350,3 +356,64 @@ def test_mtp_verify_ex_every_mode(sampler, oracle):
             want, ac = _mtp_expect(oracle, t[b], d[b], dids[b], tp[b:b + 1], dp[b:b + 1], us[b], ob, D)
             assert g_ids[b, : g_n[b]].tolist() == want and g_ac[b] == ac, (mm, nm, dc, b)
     log("mtp_verify_ex: all 12 mode combinations match")
+
+
+LAWS = ["topk_topp", "topp_only", "minp_only", "unfiltered", "topk_option", "wide_bf16", "flat_wide"]
+
+
+@pytest.mark.parametrize("law", LAWS)
+def test_mtp_verify_production_target_law(sampler, oracle, law):
+    """axs_mtp_verify_ex with AXS_MTP_TARGET_FILTERED: the acceptance test's
+    p(d) is the runner's production law (compute_mtp_target_probs +
+    extract_cpu_into + filtered_target_token_probability) in each of its
+    cases — the top-k set (the target's top_k or the target_topk option),
+    top-p only (the whole sorted row), min-p only (FullRows) and no filter
+    (the softmax value) — against the oracle's mtp_accept_count with the
+    oracle's mtp_target_prob."""
+    import torch
+
+    from ax_sampler import _abi
+
+    V = 151936 if law in ("wide_bf16", "flat_wide") else 4099
+    rng, t, d, tp, dp = _ex_case(70 + LAWS.index(law), B=12 if law != "flat_wide" else 4, V=V)
+    if law == "flat_wide":
+        # nearly flat rows: the 0.95 nucleus holds ~140k values (the sorted
+        # walk runs ~35 chunks)
+        t = (t * np.float32(0.05)).astype(np.float32)
+        d = (t[:, :-1, :] + rng.standard_normal(d.shape, dtype=np.float32) * np.float32(0.01)).astype(np.float32)
+    dtype = DTYPE_BF16 if law == "wide_bf16" else DTYPE_F32
+    if dtype == DTYPE_BF16:
+        t, d = f32_to_bf16_bits(t), f32_to_bf16_bits(d)
+    opts = {"model_mode": _abi.MTP_MODEL_REJECTION, "target_law": _abi.MTP_TARGET_FILTERED}
+    for pp in (tp, dp):
+        if law in ("topp_only", "wide_bf16", "flat_wide"):
+            pp["top_k"] = 0
+        elif law == "minp_only":
+            pp["top_k"], pp["top_p"], pp["has_min_p"], pp["min_p"] = 0, 1.0, 1, 0.05
+        elif law == "unfiltered":
+            pp["top_k"], pp["top_p"] = 0, 1.0
+        elif law == "topk_option":
+            pp["top_k"] = 0
+    if law == "topk_option":
+        opts["target_topk"] = 32
+    B, D1, _ = t.shape
+    D = D1 - 1
+    dids = _draft_ids(oracle, d, dtype, B, D, V, dp, 63)
+    us = rng.random((B, D + 1)).astype(np.float32)
+    res = sampler.mtp_verify(_to_dev(t, dtype), _to_dev(d, dtype), dids, tp, dp, uniforms=us, options=opts)
+    torch.cuda.synchronize()
+    g_ids, g_n, g_ac, g_fl = res.numpy()
+    near = 0
+    tf = bf16_bits_to_f32(t) if dtype == DTYPE_BF16 else t
+    df = bf16_bits_to_f32(d) if dtype == DTYPE_BF16 else d
+    for b in range(B):
+        ob = {k: (v[b] if isinstance(v, np.ndarray) else v) for k, v in opts.items()}
+        want, ac = _mtp_expect(oracle, tf[b], df[b], dids[b], tp[b:b + 1], dp[b:b + 1], us[b], ob, D)
+        assert not g_fl[b] & np.uint32(_abi.MTP_FLAG_ERROR), (law, b, "declined")
+        if g_fl[b] & np.uint32(_abi.MTP_FLAG_NEAR_ACCEPT):
+            near += 1
+            continue
+        got = g_ids[b, : g_n[b]].tolist()
+        assert got == want and g_ac[b] == ac, (law, b, got, want, int(g_ac[b]), ac, hex(int(g_fl[b])))
+    assert near <= boundary_allowance(B), near
+    log(f"mtp production target law {law}: {B} sequences, near {near}, accepted {int(g_ac.sum())}")

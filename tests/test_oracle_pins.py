@@ -616,3 +616,50 @@ def test_mtp_draft_stochastic_mode_inverts_the_softmax_cdf(oracle, seed):
     tok, lnq, _ = oracle.mtp_draft(x, 0.0, oracle.MTP_DRAFT_STOCHASTIC, 0.3)
     assert tok == int(np.argmax(x))
     assert abs(lnq - _log_softmax64(x, 1.0)[tok]) < 1e-5
+
+
+def _prod_law64(x, tok, T, top_p, top_k, min_p, topk_opt):
+    """The production target law in float64 (runner/mod.rs:11836-12159), for
+    tiny rows; returns (P, margin of the top-p cut)."""
+    z = (x.astype(np.float64) - x.max()) / T
+    p = np.exp(z) / np.exp(z).sum()
+    if topk_opt == 0 and top_k == 0 and not top_p < 1.0 and min_p is None:
+        return p[tok], np.inf
+    V = x.size
+    K = min(topk_opt, V) if topk_opt else (min(top_k, V) if (top_k and top_k < V) else V)
+    tp = top_p if (topk_opt or top_k or top_p < 1.0) else 1.0
+    order = np.lexsort((np.arange(V), -p))[:K]
+    if min_p is not None:
+        order = order[p[order] >= min_p * p[order[0]]]
+    margin = np.inf
+    if 0.0 < tp < 1.0:
+        cum = np.cumsum(p[order])
+        k = int(np.searchsorted(cum, tp))  # first cum >= tp
+        k = min(k, order.size - 1)
+        margin = np.min(np.abs(cum - tp))
+        order = order[: k + 1]
+    return (p[tok] / p[order].sum() if tok in order else 0.0), margin
+
+
+@pytest.mark.parametrize("seed", range(4))
+def test_production_target_law_matches_float64_statement(oracle, seed):
+    """Random tiny rows and laws: the oracle's f32 law within 1e-5 of its
+    float64 statement (rows whose top-p cut lies within 1e-5 skipped)."""
+    rng = np.random.default_rng([seed, 41])
+    checked = 0
+    for trial in range(60):
+        V = int(rng.integers(2, 40))
+        x = np.round(rng.standard_normal(V) * 2.0, 2).astype(np.float32)
+        T = float(rng.choice([0.5, 1.0, 1.5]))
+        top_p = float(rng.choice([1.0, 0.9, 0.6, 0.3]))
+        top_k = int(rng.choice([0, 0, 3, 10]))
+        min_p = [None, 0.05, 0.3][int(rng.integers(0, 3))]
+        topk_opt = int(rng.choice([0, 0, 0, 5]))
+        tok = int(rng.integers(0, V))
+        want, margin = _prod_law64(x, tok, T, top_p, top_k, min_p, topk_opt)
+        if margin < 1e-5:
+            continue
+        got = oracle.mtp_target_prob(x, tok, T, top_p, top_k, min_p, topk_opt)
+        assert abs(got - want) < 1e-5, (seed, trial, got, want)
+        checked += 1
+    assert checked > 50

@@ -400,3 +400,43 @@ def test_soft_close_probe_edge_cases(oracle):
     assert not oracle.soft_close_in_top_k([1.0, 2.0], 0, 0)
     assert not oracle.soft_close_in_top_k([1.0, 2.0], 9, 3)
     assert oracle.soft_close_in_top_k([1.0, 2.0], 0, 3)
+
+
+def test_production_target_law_four_sevenths(oracle):
+    # runner/mod.rs:20086-20125 (filtered_target_probs_match_gpu_topk_full_probability_sampler):
+    # row ln(.4,.3,.2,.1), target top_p 0.55, top_k 2 -> p(0) = 4/7, p(1) = 3/7
+    row = np.log(np.array([0.4, 0.3, 0.2, 0.1], dtype=np.float32)).astype(np.float32)
+    assert abs(oracle.mtp_target_prob(row, 0, 1.0, top_p=0.55, top_k=2) - 4.0 / 7.0) < 1e-6
+    assert abs(oracle.mtp_target_prob(row, 1, 1.0, top_p=0.55, top_k=2) - 3.0 / 7.0) < 1e-6
+
+
+def test_production_target_law_out_of_top_k_set_is_zero(oracle):
+    # runner/mod.rs:20032-20083 (topk_target_softmax_returns_zero_for_out_of_set_tokens)
+    row = np.zeros(100, np.float32)
+    row[:3] = [10.0, 9.0, 8.0]
+    assert oracle.mtp_target_prob(row, 99, 0.8, topk_opt=3) == 0.0
+    assert oracle.mtp_target_prob(row, 0, 0.8, topk_opt=3) > 0.5
+
+
+def test_production_target_law_top_k_option_approximates_full(oracle):
+    # runner/mod.rs:19937-20029 (topk_target_softmax_approximates_full_softmax_for_dominant_tokens)
+    vocab = 100
+    rows = np.zeros((3, vocab), np.float32)
+    rows[0, 10], rows[0, 20] = 5.0, 4.0
+    rows[1, 25], rows[1, 30] = 6.0, 3.0
+    rows[2, 55], rows[2, 60] = 7.0, 2.0
+    for i, tok in enumerate([10, 25, 55]):
+        full = oracle.mtp_target_prob(rows[i], tok, 0.8)
+        topk = oracle.mtp_target_prob(rows[i], tok, 0.8, topk_opt=32)
+        assert full > 0.0 and topk > 0.0
+        assert 0.85 <= topk / full < 1.15
+
+
+def test_production_target_law_min_p_full_rows(oracle):
+    # runner/mod.rs:14069-14080 (filtered_target_token_probability_applies_min_p):
+    # probs .9/.05/.05, min_p .1 -> p(0) = 1, p(1) = 0; without min_p, .9
+    row = np.log(np.array([0.9, 0.05, 0.05], dtype=np.float32)).astype(np.float32)
+    assert abs(oracle.mtp_target_prob(row, 0, 1.0, min_p=0.1) - 1.0) < 1e-5
+    assert oracle.mtp_target_prob(row, 1, 1.0, min_p=0.1) == 0.0
+    assert abs(oracle.mtp_target_prob(row, 0, 1.0) - 0.9) < 1e-5
+    assert np.isnan(oracle.mtp_target_prob(row, 0, 0.0))
