@@ -87,15 +87,22 @@ struct LmArgs {
     float inv_cap, cap;      // cap <= 0: off
     float* out;              // [B, os] f32 or null
     int64_t os;
+    int out_vec;             // out 16-byte aligned and os % 4 == 0: 16-byte stores
     unsigned long long* keys;  // [B] argmax keys (zeroed by the caller) or null
 };
 
-// Epilogue shared by both kernels: bf16 rounding, scale, softcap, the
-// store, and the argmax key of one logit (0 when v is past V).
-__device__ __forceinline__ unsigned long long finish_logit(const LmArgs& a, float acc, int v, float* orow) {
+// Epilogue shared by both kernels: bf16 rounding, scale and softcap of one
+// logit.
+__device__ __forceinline__ float logit_of(const LmArgs& a, float acc) {
     float x = bf16_round(acc);
     if (a.scale != 1.0f) x = x * a.scale;
     if (a.cap > 0.0f) x = tanhf(x * a.inv_cap) * a.cap;
+    return x;
+}
+
+// ... with its store and its argmax key (0 when v is past V).
+__device__ __forceinline__ unsigned long long finish_logit(const LmArgs& a, float acc, int v, float* orow) {
+    const float x = logit_of(a, acc);
     if (v >= a.V) return 0ull;
     if (orow) orow[v] = x;
     return am_key(x, (uint32_t)v);
@@ -314,13 +321,27 @@ __global__ __launch_bounds__(NT) void k_lm_head_mfma(LmArgs a) {
         const int b = b0 + 16 * nb + r16;
         float* orow = (a.out && b < a.B) ? a.out + (int64_t)b * a.os : nullptr;
 #pragma unroll
-        for (int m = 0; m < WR; ++m)
+        for (int m = 0; m < WR; ++m) {
+            // this lane's 4 consecutive ids of the block: one 16-byte store
+            // when the row allows it
+            const int vq = v0 + 16 * (wave + 4 * m) + 4 * g;
+            float x[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const int v = v0 + 16 * (wave + 4 * m) + 4 * g + i;
-                const unsigned long long k = finish_logit(a, acc[m][nb][i], v, orow);
+                x[i] = logit_of(a, acc[m][nb][i]);
+                const unsigned long long k = vq + i < a.V ? am_key(x[i], (uint32_t)(vq + i)) : 0ull;
                 best[nb] = (b < a.B && k > best[nb]) ? k : best[nb];
             }
+            if (orow) {
+                if (a.out_vec && vq + 4 <= a.V) {
+                    *reinterpret_cast<f32x4*>(orow + vq) = f32x4{x[0], x[1], x[2], x[3]};
+                } else {
+#pragma unroll
+                    for (int i = 0; i < 4; ++i)
+                        if (vq + i < a.V) orow[vq + i] = x[i];
+                }
+            }
+        }
     }
     if (!a.keys) return;
     __shared__ unsigned long long s_key[NT / 64][BMAX];

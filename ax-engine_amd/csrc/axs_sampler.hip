@@ -5537,6 +5537,7 @@ int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, con
     a.inv_cap = softcap > 0.0f ? 1.0f / softcap : 0.0f;
     a.out = out_logits;
     a.os = out_stride;
+    a.out_vec = (out_logits && ((uintptr_t)out_logits & 15) == 0 && out_stride % 4 == 0) ? 1 : 0;
     a.keys = out_argmax ? (unsigned long long*)ctx->tmp64 : nullptr;
     if (a.keys) {
         hipLaunchKernelGGL(k_fill_u32, dim3((2 * batch + 255) / 256), dim3(256), 0, s, (uint32_t*)a.keys,

@@ -94,3 +94,23 @@ def test_error_handler_and_last_error_without_a_gpu():
     L.axs_set_error_handler(HANDLER(), None)
     assert L.axs_context_create(0, 10, -1, ctypes.byref(out)) == 1
     assert len(seen) == 1
+
+
+def test_new_entry_points_refuse_bad_arguments_without_a_gpu():
+    """axs_lm_head and axs_mtp_draft validate their arguments before any HIP
+    call: a NULL context or a shape they cannot take is AXS_E_INVALID with a
+    message, on a machine without a GPU."""
+    from ax_sampler import _abi
+
+    L = ctypes.CDLL(_abi.LIB_PATH)
+    L.axs_last_error.restype = ctypes.c_char_p
+    vp, i32, i64, f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+    L.axs_lm_head.restype = i32
+    L.axs_lm_head.argtypes = [vp, vp, i64, vp, i64, i32, i32, i32, f32, f32, vp, i64, vp, vp]
+    L.axs_mtp_draft.restype = i32
+    L.axs_mtp_draft.argtypes = [vp, vp, i32, i32, i32, i64, vp, i32, vp, vp, vp, vp]
+    p = ctypes.c_void_p(16)  # never dereferenced: refused first
+    assert L.axs_lm_head(None, p, 64, p, 64, 1, 64, 10, 1.0, 0.0, p, 10, p, None) == 1
+    assert b"non-NULL" in L.axs_last_error()
+    assert L.axs_mtp_draft(None, p, 0, 1, 10, 10, p, 0, None, p, p, None) == 1
+    assert b"non-NULL" in L.axs_last_error()
