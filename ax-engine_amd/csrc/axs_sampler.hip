@@ -187,15 +187,6 @@ struct KArgs {
     uint32_t topn;
     uint32_t* topn_ids;  // [rows, topn]
     float* topn_lp;      // [rows, topn]
-    // production target-probability rows (axs_mtp_verify_ex with
-    // AXS_MTP_TARGET_FILTERED): the target rows b * prod_d1 + i of a verify
-    // batch, each with the draft token of position i < prod_d1 - 1 in
-    // lp_tokens; prod_out[b, i] receives that token's target probability
-    const axs_sampling_params* prod_params;  // [batch] the target's params
-    float* prod_out;                         // [batch, prod_d1 - 1]
-    uint32_t prod_topk;                      // mtp_target_softmax_topk (0: none)
-    int32_t prod_d1;
-    float* mtp_ptgt;  // k_mtp_verify: [batch, depth] target probabilities of the draft tokens, or NULL
     // MTP verify options (axs_mtp_verify_ex); mtp_stream: uniforms in the
     // reference's stream order (else the slot layout of axs_mtp_verify)
     const uint32_t* mtp_sources;  // [batch, depth] or NULL
@@ -3709,167 +3700,6 @@ __device__ __forceinline__ void exact_row(const KArgs& a, int r, const RowState&
         }
         return;
     }
-    if (a.lp_tokens && a.prod_out) {
-        // Production target law of a draft token (compute_mtp_target_probs,
-        // runner/mod.rs:12025-12159, then extract_cpu_into, :11836-11937, and
-        // filtered_target_token_probability, :11943-12001) over this row's
-        // softmax p_j = q_j / S (full_vocab_token_logprob's terms and
-        // index-order sum).  The filtered laws keep the K largest p
-        // ((p desc, id asc)), those >= min_p * max p, cut where the f32
-        // running sum in that order first reaches top_p, and divide p_t by the
-        // kept sum in that order.  Only values enter the sums, so the sorted
-        // values are walked in chunks of PROD_CAP: each chunk's values found
-        // by a radix select of its last position's value (4 passes of 8 bits
-        // over the row), gathered into LDS, sorted and summed by the exact
-        // block scan from the previous chunk's sum, until the running sum
-        // reaches top_p or the kept prefix ends; t's place in the order is
-        // counted over the row.
-        constexpr uint32_t PROD_CAP = 4096;
-        const uint32_t d1 = (uint32_t)a.prod_d1, bq = (uint32_t)r / d1, iq = (uint32_t)r % d1;
-        if (iq + 1u >= d1) return;  // the bonus row has no draft position
-        const axs_sampling_params pp = a.prod_params[bq];
-        const uint32_t t = a.lp_tokens[r];
-        const float Z = S[V - 1];
-        float* slot = a.prod_out + (size_t)bq * (d1 - 1u) + iq;
-        if (!(Z > 0.0f) || !isfinite(Z) || t >= V) {
-            if (tid == 0) *slot = 0.0f;
-            return;
-        }
-        auto pv = [&](uint32_t j) { return __fdiv_rn(dense[j], Z); };
-        const bool mp_on = pp.has_min_p && isfinite(pp.min_p) && pp.min_p > 0.0f;
-        if (a.prod_topk == 0 && pp.top_k == 0 && !(pp.top_p < 1.0f) && !mp_on) {
-            if (tid == 0) *slot = pv(t);  // the softmax value itself
-            return;
-        }
-        uint32_t K = V;
-        float tp = pp.top_p;
-        if (a.prod_topk > 0) K = a.prod_topk < V ? a.prod_topk : V;
-        else if (pp.top_k > 0 || pp.top_p < 1.0f) K = (pp.top_k > 0 && pp.top_k < V) ? pp.top_k : V;
-        else tp = 1.0f;
-        const bool cut = isfinite(tp) && tp > 0.0f && tp < 1.0f;
-        const float ptok = pv(t);
-        float lmax = 0.0f;
-        for (uint32_t j = tid; j < V; j += NT_EX) lmax = fmaxf(lmax, pv(j));
-        const float pmax = block_max<NT_EX>(lmax, reinterpret_cast<float*>(s_u));
-        const float cutoff = mp_on ? __fmul_rn(pp.min_p, pmax) : 0.0f;
-        uint32_t cm = 0, cgt = 0, ceq = 0;
-        for (uint32_t j = tid; j < V; j += NT_EX) {
-            const float q = pv(j);
-            cm += (q > 0.0f && q >= cutoff) ? 1u : 0u;
-            cgt += q > ptok ? 1u : 0u;
-            ceq += (q == ptok && j < t) ? 1u : 0u;
-        }
-        const uint32_t n_m = block_sum_u32<NT_EX>(cm, s_u);
-        const uint32_t rank_t = block_sum_u32<NT_EX>(cgt, s_u) + block_sum_u32<NT_EX>(ceq, s_u);
-        const uint32_t Kp = n_m < K ? n_m : K;
-        if (Kp == 0) {
-            if (tid == 0) *slot = 0.0f;
-            return;
-        }
-        // The sorted values in chunks of up to PROD_CAP: the chunk ending at
-        // sorted position `end` is everything above the end-th largest bit
-        // pattern th (p >= 0: bits order as values) plus `want` copies of it,
-        // minus what the previous chunks took (above th0, plus want0 copies
-        // of th0).
-        uint32_t* hist = s_cnt;
-        uint64_t* vk = reinterpret_cast<uint64_t*>(s_cnt + 512);           // PROD_CAP sort keys
-        float* Ss = reinterpret_cast<float*>(s_cnt + 512 + 2 * PROD_CAP);  // running sums
-        auto select = [&](uint32_t rank, uint32_t& th, uint32_t& want) {
-            uint32_t prefix = 0, mask = 0;
-            want = rank;
-            for (int shift = 24; shift >= 0; shift -= 8) {
-                for (uint32_t j = tid; j < 256u; j += NT_EX) hist[j] = 0;
-                __syncthreads();
-                for (uint32_t j = tid; j < V; j += NT_EX) {
-                    const uint32_t bb = __float_as_uint(pv(j));
-                    if ((bb & mask) == prefix && bb != 0u) atomicAdd(&hist[(bb >> shift) & 255u], 1u);
-                }
-                __syncthreads();
-                if (tid == 0) {
-                    uint32_t cum = 0, dg = 0;
-                    for (int q = 255; q >= 0; --q) {
-                        if (cum + hist[q] >= want) {
-                            dg = (uint32_t)q;
-                            break;
-                        }
-                        cum += hist[q];
-                    }
-                    s_k = dg;
-                    s_cross = want - cum;
-                }
-                __syncthreads();
-                prefix |= s_k << shift;
-                mask |= 255u << shift;
-                want = s_cross;
-                __syncthreads();
-            }
-            th = prefix;
-        };
-        uint32_t pos = 0, th0 = 0xFFFFFFFFu, want0 = 0, keep = Kp;
-        float run = 0.0f, fsum = 0.0f;
-        bool found = false;
-        while (pos < Kp) {
-            const uint32_t end = (Kp - pos > PROD_CAP) ? pos + PROD_CAP : Kp;
-            const uint32_t nch = end - pos;
-            uint32_t th, want;
-            select(end, th, want);
-            // copies of th0 left after the previous chunks
-            if (tid == 0) s_k = 0;
-            __syncthreads();
-            uint32_t ce = 0;
-            for (uint32_t j = tid; j < V; j += NT_EX) ce += __float_as_uint(pv(j)) == th0 ? 1u : 0u;
-            const uint32_t n_th0 = block_sum_u32<NT_EX>(ce, s_u);
-            // strictly between th and th0
-            for (uint32_t j = tid; j < V; j += NT_EX) {
-                const uint32_t bb = __float_as_uint(pv(j));
-                if (bb > th && bb < th0) vk[atomicAdd(&s_k, 1u)] = (uint64_t)bb << 32;
-            }
-            __syncthreads();
-            uint32_t ng = s_k;
-            const uint32_t c_hi = th < th0 ? (pos > 0 ? n_th0 - want0 : 0u) : 0u;  // th0's remaining copies
-            const uint32_t c_lo = th < th0 ? want : want - want0;                  // copies of th in this chunk
-            const uint32_t np2 = next_pow2(nch);
-            for (uint32_t j = ng + (uint32_t)tid; j < np2; j += NT_EX) {
-                uint64_t kv = 0ull;
-                if (j < ng + c_hi) kv = (uint64_t)th0 << 32;
-                else if (j < ng + c_hi + c_lo) kv = (uint64_t)th << 32;
-                vk[j] = kv;
-            }
-            __threadfence_block();
-            __syncthreads();
-            block_sort_desc<NT_EX>(vk, np2);
-            block_exact_sums<XI>([&](uint32_t k) { return __uint_as_float((uint32_t)(vk[k] >> 32)); }, 0u, nch,
-                                 run, Ss, XL.sum);
-            __threadfence_block();
-            __syncthreads();
-            if (cut) {
-                // the first running sum reaching top_p
-                if (tid == 0) s_k = NONE;
-                __syncthreads();
-                uint32_t first = NONE;
-                for (uint32_t k = tid; k < nch; k += NT_EX)
-                    if (Ss[k] >= tp) first = min(first, k);
-                if (first != NONE) atomicMin(&s_k, first);
-                __syncthreads();
-                const uint32_t fk = s_k;
-                __syncthreads();
-                if (fk != NONE) {
-                    keep = pos + fk + 1u;
-                    fsum = Ss[fk];
-                    found = true;
-                    break;
-                }
-            }
-            run = Ss[nch - 1u];
-            th0 = th;
-            want0 = want;  // copies of th among the first `end` positions
-            pos = end;
-        }
-        if (!found) fsum = run;  // every kept value summed
-        if (tid == 0)
-            *slot = (ptok > 0.0f && rank_t < keep) ? fmaxf(__fdiv_rn(ptok, fmaxf(fsum, 1e-37f)), 0.0f) : 0.0f;
-        return;
-    }
     if (a.lp_tokens) {
         // token-logprob row: max(ln(max(p_t / S, 1e-37)), -30) with S the
         // index-order f32 sum (crates/ax-engine-mlx/src/sampling.rs:772-786)
@@ -4164,7 +3994,8 @@ constexpr int NT_MTP = 1024;
 // test and slot D for the tail (axs_mtp_verify).
 __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* draft_ids,
                                                        uint32_t* out_ids, uint32_t* out_count,
-                                                       uint32_t* out_accept, uint32_t* out_flags) {
+                                                       uint32_t* out_accept, uint32_t* out_flags,
+                                                       const float* ptgt) {
     __shared__ uint64_t s_t[KEPT_CAP];
     __shared__ uint64_t s_d[KEPT_CAP];
     __shared__ float s_v[KEPT_CAP];     // residual terms (then their normalised values) in walk order
@@ -4260,7 +4091,7 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
         const float rawd = has_dd ? praw(dr, rd, big_d, dp_l, s_fd) : -1.0f;
         // normalised entries p / F (TokenDistribution::new, sampling.rs:128-144)
         float pt = fmaxf(rawt >= 0.0f ? __fdiv_rn(rawt, rt.F) : 0.0f, 0.0f);
-        if (a.mtp_ptgt) pt = a.mtp_ptgt[(size_t)b * D + i];  // the production law's, formed before the pipeline
+        if (ptgt) pt = ptgt[(size_t)b * D + i];  // the production law's (k_mtp_prod), or P_i(d)
         float lnq;
         if (a.mtp_lnq_in) {
             lnq = a.mtp_lnq_in[(size_t)b * D + i];
@@ -4534,6 +4365,195 @@ __global__ __launch_bounds__(NT_MTP) void k_mtp_verify(KArgs a, const uint32_t* 
     out_count[b] = count;
     if (out_accept) out_accept[b] = acc;
     if (out_flags) out_flags[b] = flags;
+}
+
+// --------------------------------------------------------------------------
+// k_mtp_prod: the production target law's p(d) of each draft token
+// (axs_mtp_verify_ex with AXS_MTP_TARGET_FILTERED), one workgroup per target
+// row r = b * d1 + i of the verify batch, run right after the index-order
+// exact pass over those rows has left each row's softmax terms (dense) and
+// their index-order sum (S[V - 1]) in the workspace.
+// --------------------------------------------------------------------------
+struct ProdArgs {
+    const uint32_t* tokens;            // [rows] the draft token of each target row
+    const axs_sampling_params* params; // [batch] the target's params
+    float* out;                        // [batch, d1 - 1]
+    uint32_t topk;                     // mtp_target_softmax_topk (0: none)
+    int32_t d1;                        // depth + 1
+};
+
+__global__ __launch_bounds__(NT_EX) void k_mtp_prod(KArgs a, ProdArgs pa) {
+    __shared__ ExLds XL;
+    uint32_t* s_cnt = XL.cnt;
+    uint32_t* s_u = XL.u;
+    uint32_t &s_k = XL.k, &s_cross = XL.cross;
+    const int tid = threadIdx.x;
+    const int r = blockIdx.x;
+    const uint32_t V = (uint32_t)a.vocab;
+    const float* dense = a.dense + (size_t)r * V;
+    const float* S = a.sbuf + (size_t)r * V;
+    // a row the pass decided without the exact path (T <= 0, an id past the
+    // vocabulary, no finite maximum) left S[V - 1] at the 0 it was given
+    // before the pass, and its slot keeps 0
+        // Production target law of a draft token (compute_mtp_target_probs,
+        // runner/mod.rs:12025-12159, then extract_cpu_into, :11836-11937, and
+        // filtered_target_token_probability, :11943-12001) over this row's
+        // softmax p_j = q_j / S (full_vocab_token_logprob's terms and
+        // index-order sum).  The filtered laws keep the K largest p
+        // ((p desc, id asc)), those >= min_p * max p, cut where the f32
+        // running sum in that order first reaches top_p, and divide p_t by the
+        // kept sum in that order.  Only values enter the sums, so the sorted
+        // values are walked in chunks of PROD_CAP: each chunk's values found
+        // by a radix select of its last position's value (4 passes of 8 bits
+        // over the row), gathered into LDS, sorted and summed by the exact
+        // block scan from the previous chunk's sum, until the running sum
+        // reaches top_p or the kept prefix ends; t's place in the order is
+        // counted over the row.
+        constexpr uint32_t PROD_CAP = 4096;
+        const uint32_t d1 = (uint32_t)pa.d1, bq = (uint32_t)r / d1, iq = (uint32_t)r % d1;
+        if (iq + 1u >= d1) return;  // the bonus row has no draft position
+        const axs_sampling_params pp = pa.params[bq];
+        const uint32_t t = pa.tokens[r];
+        const float Z = S[V - 1];
+        float* slot = pa.out + (size_t)bq * (d1 - 1u) + iq;
+        if (!(Z > 0.0f) || !isfinite(Z) || t >= V) {
+            if (tid == 0) *slot = 0.0f;
+            return;
+        }
+        auto pv = [&](uint32_t j) { return __fdiv_rn(dense[j], Z); };
+        const bool mp_on = pp.has_min_p && isfinite(pp.min_p) && pp.min_p > 0.0f;
+        if (pa.topk == 0 && pp.top_k == 0 && !(pp.top_p < 1.0f) && !mp_on) {
+            if (tid == 0) *slot = pv(t);  // the softmax value itself
+            return;
+        }
+        uint32_t K = V;
+        float tp = pp.top_p;
+        if (pa.topk > 0) K = pa.topk < V ? pa.topk : V;
+        else if (pp.top_k > 0 || pp.top_p < 1.0f) K = (pp.top_k > 0 && pp.top_k < V) ? pp.top_k : V;
+        else tp = 1.0f;
+        const bool cut = isfinite(tp) && tp > 0.0f && tp < 1.0f;
+        const float ptok = pv(t);
+        float lmax = 0.0f;
+        for (uint32_t j = tid; j < V; j += NT_EX) lmax = fmaxf(lmax, pv(j));
+        const float pmax = block_max<NT_EX>(lmax, reinterpret_cast<float*>(s_u));
+        const float cutoff = mp_on ? __fmul_rn(pp.min_p, pmax) : 0.0f;
+        uint32_t cm = 0, cgt = 0, ceq = 0;
+        for (uint32_t j = tid; j < V; j += NT_EX) {
+            const float q = pv(j);
+            cm += (q > 0.0f && q >= cutoff) ? 1u : 0u;
+            cgt += q > ptok ? 1u : 0u;
+            ceq += (q == ptok && j < t) ? 1u : 0u;
+        }
+        const uint32_t n_m = block_sum_u32<NT_EX>(cm, s_u);
+        const uint32_t rank_t = block_sum_u32<NT_EX>(cgt, s_u) + block_sum_u32<NT_EX>(ceq, s_u);
+        const uint32_t Kp = n_m < K ? n_m : K;
+        if (Kp == 0) {
+            if (tid == 0) *slot = 0.0f;
+            return;
+        }
+        // The sorted values in chunks of up to PROD_CAP: the chunk ending at
+        // sorted position `end` is everything above the end-th largest bit
+        // pattern th (p >= 0: bits order as values) plus `want` copies of it,
+        // minus what the previous chunks took (above th0, plus want0 copies
+        // of th0).
+        uint32_t* hist = s_cnt;
+        uint64_t* vk = reinterpret_cast<uint64_t*>(s_cnt + 512);           // PROD_CAP sort keys
+        float* Ss = reinterpret_cast<float*>(s_cnt + 512 + 2 * PROD_CAP);  // running sums
+        auto select = [&](uint32_t rank, uint32_t& th, uint32_t& want) {
+            uint32_t prefix = 0, mask = 0;
+            want = rank;
+            for (int shift = 24; shift >= 0; shift -= 8) {
+                for (uint32_t j = tid; j < 256u; j += NT_EX) hist[j] = 0;
+                __syncthreads();
+                for (uint32_t j = tid; j < V; j += NT_EX) {
+                    const uint32_t bb = __float_as_uint(pv(j));
+                    if ((bb & mask) == prefix && bb != 0u) atomicAdd(&hist[(bb >> shift) & 255u], 1u);
+                }
+                __syncthreads();
+                if (tid == 0) {
+                    uint32_t cum = 0, dg = 0;
+                    for (int q = 255; q >= 0; --q) {
+                        if (cum + hist[q] >= want) {
+                            dg = (uint32_t)q;
+                            break;
+                        }
+                        cum += hist[q];
+                    }
+                    s_k = dg;
+                    s_cross = want - cum;
+                }
+                __syncthreads();
+                prefix |= s_k << shift;
+                mask |= 255u << shift;
+                want = s_cross;
+                __syncthreads();
+            }
+            th = prefix;
+        };
+        uint32_t pos = 0, th0 = 0xFFFFFFFFu, want0 = 0, keep = Kp;
+        float run = 0.0f, fsum = 0.0f;
+        bool found = false;
+        while (pos < Kp) {
+            const uint32_t end = (Kp - pos > PROD_CAP) ? pos + PROD_CAP : Kp;
+            const uint32_t nch = end - pos;
+            uint32_t th, want;
+            select(end, th, want);
+            // copies of th0 left after the previous chunks
+            if (tid == 0) s_k = 0;
+            __syncthreads();
+            uint32_t ce = 0;
+            for (uint32_t j = tid; j < V; j += NT_EX) ce += __float_as_uint(pv(j)) == th0 ? 1u : 0u;
+            const uint32_t n_th0 = block_sum_u32<NT_EX>(ce, s_u);
+            // strictly between th and th0
+            for (uint32_t j = tid; j < V; j += NT_EX) {
+                const uint32_t bb = __float_as_uint(pv(j));
+                if (bb > th && bb < th0) vk[atomicAdd(&s_k, 1u)] = (uint64_t)bb << 32;
+            }
+            __syncthreads();
+            uint32_t ng = s_k;
+            const uint32_t c_hi = th < th0 ? (pos > 0 ? n_th0 - want0 : 0u) : 0u;  // th0's remaining copies
+            const uint32_t c_lo = th < th0 ? want : want - want0;                  // copies of th in this chunk
+            const uint32_t np2 = next_pow2(nch);
+            for (uint32_t j = ng + (uint32_t)tid; j < np2; j += NT_EX) {
+                uint64_t kv = 0ull;
+                if (j < ng + c_hi) kv = (uint64_t)th0 << 32;
+                else if (j < ng + c_hi + c_lo) kv = (uint64_t)th << 32;
+                vk[j] = kv;
+            }
+            __threadfence_block();
+            __syncthreads();
+            block_sort_desc<NT_EX>(vk, np2);
+            block_exact_sums<8>([&](uint32_t k) { return __uint_as_float((uint32_t)(vk[k] >> 32)); }, 0u, nch,
+                                 run, Ss, XL.sum);
+            __threadfence_block();
+            __syncthreads();
+            if (cut) {
+                // the first running sum reaching top_p
+                if (tid == 0) s_k = NONE;
+                __syncthreads();
+                uint32_t first = NONE;
+                for (uint32_t k = tid; k < nch; k += NT_EX)
+                    if (Ss[k] >= tp) first = min(first, k);
+                if (first != NONE) atomicMin(&s_k, first);
+                __syncthreads();
+                const uint32_t fk = s_k;
+                __syncthreads();
+                if (fk != NONE) {
+                    keep = pos + fk + 1u;
+                    fsum = Ss[fk];
+                    found = true;
+                    break;
+                }
+            }
+            run = Ss[nch - 1u];
+            th0 = th;
+            want0 = want;  // copies of th among the first `end` positions
+            pos = end;
+        }
+        if (!found) fsum = run;  // every kept value summed
+        if (tid == 0)
+            *slot = (ptok > 0.0f && rank_t < keep) ? fmaxf(__fdiv_rn(ptok, fmaxf(fsum, 1e-37f)), 0.0f) : 0.0f;
+        return;
 }
 
 // --------------------------------------------------------------------------
@@ -5681,6 +5701,13 @@ __global__ void k_prod_prep(const uint32_t* draft_ids, const axs_sampling_params
     temps[q] = tp[b].temperature;
 }
 
+// the last running-sum slot of rows [0, n) set to 0: a row the exact path
+// does not reach keeps it
+__global__ void k_zero_last(float* S, int n, uint32_t V) {
+    const int q = blockIdx.x * blockDim.x + threadIdx.x;
+    if (q < n) S[(size_t)q * V + V - 1u] = 0.0f;
+}
+
 int mtp_verify_impl(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_options* op,
                     const axs_mtp_outputs* o, void* stream) {
     if (!ctx || !d || !o) return fail(AXS_E_INVALID, "ctx, desc and outputs must be non-NULL");
@@ -5724,13 +5751,19 @@ int mtp_verify_impl(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_optio
         l.params = nullptr;
         l.lp_tokens = ctx->lp_tok;
         l.lp_temps = ctx->lp_temps;
-        l.prod_params = d->target_params;
-        l.prod_out = ctx->mtp_ptgt;
-        l.prod_topk = op->target_topk;
-        l.prod_d1 = d->depth + 1;
         l.out_ids = ctx->mtp_amax;  // the rows' tokens echoed: scratch
+        hipLaunchKernelGGL(k_zero_last, dim3((unsigned)((nt + 255) / 256)), dim3(256), 0, s, ctx->sbuf, nt,
+                           (uint32_t)d->vocab);
         Plan lpp = make_plan(d->dtype, nt, d->vocab, d->target_logits, d->row_stride, nullptr);
         if ((rc = run_pipeline(ctx, l, lpp, s))) return rc;
+        ProdArgs pa{};
+        pa.tokens = ctx->lp_tok;
+        pa.params = d->target_params;
+        pa.out = ctx->mtp_ptgt;
+        pa.topk = op->target_topk;
+        pa.d1 = d->depth + 1;
+        hipLaunchKernelGGL(k_mtp_prod, dim3((unsigned)nt), dim3(NT_EX), 0, s, l, pa);
+        AXS_HIP_CHECK(hipGetLastError());
     }
     if (full_lnq) {
         // ln softmax(draft row / T_d)[d] of every draft row, the draft's own
@@ -5775,7 +5808,6 @@ int mtp_verify_impl(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_optio
         a.mtp_lnq_in = op->pending_log_probs;
         a.mtp_pred = op->predicted;
         a.mtp_lnq_full = full_lnq ? ctx->mtp_lnq : nullptr;
-        a.mtp_ptgt = prod ? ctx->mtp_ptgt : nullptr;
         a.mtp_model_mode = op->model_mode;
         a.mtp_ngram_mode = op->ngram_mode;
         a.mtp_delta = op->delta_correction ? 1 : 0;
@@ -5786,7 +5818,7 @@ int mtp_verify_impl(axs_context* ctx, const axs_mtp_desc* d, const axs_mtp_optio
     if ((rc = run_pipeline(ctx, a, pl, s))) return rc;
     timed(ctx, AXS_KERNEL_MTP, s, [&] {
         hipLaunchKernelGGL(k_mtp_verify, dim3((unsigned)d->batch), dim3(NT_MTP), 0, s, a, d->draft_ids,
-                           o->out_ids, o->out_count, o->accept_count, o->flags);
+                           o->out_ids, o->out_count, o->accept_count, o->flags, prod ? ctx->mtp_ptgt : nullptr);
     });
     AXS_HIP_CHECK(hipGetLastError());
     return order_end(ctx, s);
