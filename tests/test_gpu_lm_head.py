@@ -184,3 +184,7 @@ def test_lm_head_rejects_bad_shapes(sampler):
     weight = torch.zeros((10, 100), dtype=torch.bfloat16, device="cuda:0")
     with pytest.raises(SamplerError):
         sampler.lm_head(hidden, weight)  # H % 32 != 0
+    hidden = torch.zeros((129, 64), dtype=torch.bfloat16, device="cuda:0")
+    weight = torch.zeros((10, 64), dtype=torch.bfloat16, device="cuda:0")
+    with pytest.raises(SamplerError, match="larger than the context"):
+        sampler.lm_head(hidden, weight)  # more rows than the context's max_batch (128)

@@ -358,7 +358,8 @@ def test_mtp_verify_ex_every_mode(sampler, oracle):
     log("mtp_verify_ex: all 12 mode combinations match")
 
 
-LAWS = ["topk_topp", "topp_only", "minp_only", "unfiltered", "topk_option", "wide_bf16", "flat_wide"]
+LAWS = ["topk_topp", "topp_only", "minp_only", "unfiltered", "topk_option", "wide_bf16", "flat_wide",
+        "topp_zero", "minp_above_one", "greedy_target"]
 
 
 @pytest.mark.parametrize("law", LAWS)
@@ -376,6 +377,12 @@ def test_mtp_verify_production_target_law(sampler, oracle, law):
 
     V = 151936 if law in ("wide_bf16", "flat_wide") else 4099
     rng, t, d, tp, dp = _ex_case(70 + LAWS.index(law), B=12 if law != "flat_wide" else 4, V=V)
+    if law == "topp_zero":
+        # every p within 2^-24 of the maximum: a sorted law that cuts nothing
+        # keeps ids the exact path lists only above that floor (such an MTP
+        # sequence on a wider row is declined, AXS_MTP_FLAG_ERROR)
+        t = (t * np.float32(0.3)).astype(np.float32)
+        d = (d * np.float32(0.3)).astype(np.float32)
     if law == "flat_wide":
         # nearly flat rows: the 0.95 nucleus holds ~140k values (the sorted
         # walk runs ~35 chunks)
@@ -394,6 +401,15 @@ def test_mtp_verify_production_target_law(sampler, oracle, law):
             pp["top_k"], pp["top_p"] = 0, 1.0
         elif law == "topk_option":
             pp["top_k"] = 0
+        elif law == "topp_zero":
+            # top_p < 1 selects the filtered law, but 0 cuts nothing there
+            # (0 < top_p < 1 gates the cut): every p renormalised
+            pp["top_k"], pp["top_p"] = 0, 0.0
+        elif law == "minp_above_one":
+            # min_p * max p above every p: nothing kept, p(d) = 0
+            pp["top_k"], pp["top_p"], pp["has_min_p"], pp["min_p"] = 0, 1.0, 1, 1.5
+    if law == "greedy_target":
+        tp["temperature"][::2] = 0.0  # no target probabilities: greedy comparisons
     if law == "topk_option":
         opts["target_topk"] = 32
     B, D1, _ = t.shape

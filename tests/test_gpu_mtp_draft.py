@@ -6,6 +6,7 @@ sampled mode and for T <= 0; the index-order categorical draw on the same
 uniform for the stochastic mode, boundary rows included) and ln q must be
 full_vocab_token_logprob of it within 1e-5 (the device reproduces that
 function's sequential sum).  Rows mix temperatures 0.6 / 1.0 / 1.4 / 0 / -1,
+a row of NaN and a row with -inf logits,
 bf16 and f32 logits, supplied uniforms (with 0 and 1) and Philox draws, and
 the drafted rows then feed axs_mtp_verify_ex as pending_log_probs.
 """
@@ -33,6 +34,8 @@ def sampler():
 def _rows(B, V, dtype, seed):
     rng = np.random.default_rng([seed, 77])
     x = (rng.standard_normal((B, V)) * 3.0).astype(np.float32)
+    x[2] = np.nan          # no finite logit: argmax 0, ln q -30
+    x[3, ::2] = -np.inf    # zero-probability ids
     if dtype == DTYPE_BF16:
         bits = x.view(np.uint32)
         bits = (bits + 0x7FFF + ((bits >> 16) & 1)) & 0xFFFF0000  # round to bf16
