@@ -55,7 +55,13 @@ fn main() {
 
     // --- Rerun triggers ---
     println!("cargo:rerun-if-changed=build.rs");
-    for f in ["axs_sampler.hip", "axs_device.h", "axs_exact_sum.h", "axs_expf.h"] {
+    for f in [
+        "axs_sampler.hip",
+        "axs_device.h",
+        "axs_exact_sum.h",
+        "axs_expf.h",
+        "axs_lm_head.h",
+    ] {
         println!("cargo:rerun-if-changed={}", src_dir.join(f).display());
     }
     let header = inc_dir.join("ax_hip_sampler.h");
