@@ -2917,21 +2917,22 @@ __global__ __launch_bounds__(NT_CHUNK) void k_exact_mat(KArgs a) {
                     xq[q] = xof(l);
                     if (!((sk >> q) & 1u) && e0 + q < hi && xq[q] >= ke.xe) cm |= 1u << q;
                 }
-                const uint32_t nc = (uint32_t)__popc(cm);
-                uint32_t incl = nc;
+                // the wave's exclusive prefix of the keys, one ballot per
+                // element slot (no cross-lane data movement); the wave's slot
+                // claim goes out before the staging
+                uint32_t so = 0, wt = 0;
 #pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const uint32_t y = (uint32_t)__shfl_up((int)incl, d, 64);
-                    if (lane >= d) incl += y;
+                for (int q = 0; q < EPVC; ++q) {
+                    const uint64_t bq = __ballot((cm >> q) & 1u);
+                    so += mbcnt64(bq);
+                    wt += (uint32_t)__popcll(bq);
                 }
-                const uint32_t wt = (uint32_t)__shfl((int)incl, 63, 64);
                 if (!wt) continue;  // wave-uniform
-                uint32_t so = incl - nc;
+                uint32_t base = 0;
+                if (lane == 0) base = atomicAdd(&s_cur, wt);
 #pragma unroll
                 for (int q = 0; q < EPVC; ++q)
                     if ((cm >> q) & 1u) stg[so++] = ((uint64_t)__float_as_uint(xq[q]) << 32) | (e0 + (uint32_t)q);
-                uint32_t base = 0;
-                if (lane == 0) base = atomicAdd(&s_cur, wt);
                 base = (uint32_t)__shfl((int)base, 0, 64);
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
