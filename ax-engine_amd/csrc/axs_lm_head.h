@@ -12,8 +12,8 @@
 // weight [V, H] (a linear layer's [out, in] layout), hidden the final-norm
 // output [B, H].
 //
-// The product is HBM-bound for every decode batch (W is read once per 64
-// batch rows; at B <= 64 a launch does at most 2B flops per weight byte, far
+// The product is HBM-bound for every decode batch (W is read once per 128
+// batch rows; at B <= 128 a launch does at most 2B flops per weight byte,
 // below gfx950's bf16 matrix-core-to-HBM ratio of ~312), so both kernels are
 // laid out for streaming W in long contiguous pieces:
 //
@@ -45,7 +45,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NT = 256;                  // threads per workgroup (4 waves)
-constexpr int BMAX = 64;                 // batch rows per launch slice (NB <= 4)
+constexpr int BMAX = 128;                // batch rows per launch slice at most (NB <= 8)
 
 // f32 -> bf16 -> f32, round to nearest even; NaN stays NaN (quieted).
 __device__ __forceinline__ float bf16_round(float x) {
@@ -215,7 +215,7 @@ __global__ __launch_bounds__(NT) void k_lm_head_dot(LmArgs a) {
 
 // ---------------------------------------------------------------------------
 // B > DOT_BMAX: matrix cores.  A workgroup owns 64 * WR vocabulary rows and
-// up to 64 batch rows (NB 16-row blocks); wave w computes vocabulary blocks
+// up to 128 batch rows (NB 16-row blocks); wave w computes vocabulary blocks
 // w, w + 4, ... (WR blocks of 16 rows) against every batch block with
 // v_mfma_f32_16x16x32_bf16 (W as the A operand: row = vocabulary id; hidden
 // as the B operand: column = batch row), so each hidden fragment read from
@@ -238,7 +238,7 @@ __global__ __launch_bounds__(NT) void k_lm_head_mfma(LmArgs a) {
     __shared__ u32x4 s_h[16 * NB * CH];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int r16 = lane & 15, g = lane >> 4;
-    const int v0 = blockIdx.x * ROWS, b0 = blockIdx.y * BMAX;
+    const int v0 = blockIdx.x * ROWS, b0 = blockIdx.y * 16 * NB;
     // load plan: flat 16-byte chunk index q = i * NT + t -> (row q / CH, chunk q % CH)
     const uint16_t* wsrc[WLD];
 #pragma unroll

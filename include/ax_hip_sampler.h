@@ -449,7 +449,7 @@ int axs_mtp_draft(axs_context* ctx, const void* logits, int dtype, int batch, in
  * axs_sample_batch over out_logits.  Requires hidden_size % 32 == 0, both
  * input strides multiples of 8 elements and 16-byte aligned inputs;
  * batch <= the context's max_batch (argmax keys live in its workspace).
- * The weight is read from HBM once per 64 batch rows. */
+ * The weight is read from HBM once per 128 batch rows. */
 int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, const void* weight,
                 int64_t weight_stride, int batch, int hidden_size, int vocab, float scale, float softcap,
                 float* out_logits, int64_t out_stride, uint32_t* out_argmax, void* stream);

@@ -35,7 +35,7 @@ pytestmark = pytest.mark.gpu
 def sampler():
     from ax_sampler import HipSampler
 
-    s = HipSampler(0, max_batch=128, max_vocab=262144)
+    s = HipSampler(0, max_batch=256, max_vocab=262144)
     yield s
     s.close()
 
@@ -104,7 +104,8 @@ def _argmax_rows(oracle, logits):
 
 
 @pytest.mark.parametrize("B,H,V,seed", [(1, 4096, 151936, 1), (2, 1056, 7777, 5), (13, 2080, 50021, 2),
-                                        (40, 1056, 9001, 6), (64, 4096, 151936, 3), (80, 1024, 32003, 4)])
+                                        (40, 1056, 9001, 6), (64, 4096, 151936, 3), (80, 1024, 32003, 4),
+                                        (200, 512, 20011, 7)])
 def test_lm_head_matches_exact_product(sampler, oracle, B, H, V, seed):
     import torch
 
@@ -184,7 +185,7 @@ def test_lm_head_rejects_bad_shapes(sampler):
     weight = torch.zeros((10, 100), dtype=torch.bfloat16, device="cuda:0")
     with pytest.raises(SamplerError):
         sampler.lm_head(hidden, weight)  # H % 32 != 0
-    hidden = torch.zeros((129, 64), dtype=torch.bfloat16, device="cuda:0")
+    hidden = torch.zeros((257, 64), dtype=torch.bfloat16, device="cuda:0")
     weight = torch.zeros((10, 64), dtype=torch.bfloat16, device="cuda:0")
     with pytest.raises(SamplerError, match="larger than the context"):
-        sampler.lm_head(hidden, weight)  # more rows than the context's max_batch (128)
+        sampler.lm_head(hidden, weight)  # more rows than the context's max_batch (256)
