@@ -4396,165 +4396,165 @@ __global__ __launch_bounds__(NT_EX) void k_mtp_prod(KArgs a, ProdArgs pa) {
     // a row the pass decided without the exact path (T <= 0, an id past the
     // vocabulary, no finite maximum) left S[V - 1] at the 0 it was given
     // before the pass, and its slot keeps 0
-        // Production target law of a draft token (compute_mtp_target_probs,
-        // runner/mod.rs:12025-12159, then extract_cpu_into, :11836-11937, and
-        // filtered_target_token_probability, :11943-12001) over this row's
-        // softmax p_j = q_j / S (full_vocab_token_logprob's terms and
-        // index-order sum).  The filtered laws keep the K largest p
-        // ((p desc, id asc)), those >= min_p * max p, cut where the f32
-        // running sum in that order first reaches top_p, and divide p_t by the
-        // kept sum in that order.  Only values enter the sums, so the sorted
-        // values are walked in chunks of PROD_CAP: each chunk's values found
-        // by a radix select of its last position's value (4 passes of 8 bits
-        // over the row), gathered into LDS, sorted and summed by the exact
-        // block scan from the previous chunk's sum, until the running sum
-        // reaches top_p or the kept prefix ends; t's place in the order is
-        // counted over the row.
-        constexpr uint32_t PROD_CAP = 4096;
-        const uint32_t d1 = (uint32_t)pa.d1, bq = (uint32_t)r / d1, iq = (uint32_t)r % d1;
-        if (iq + 1u >= d1) return;  // the bonus row has no draft position
-        const axs_sampling_params pp = pa.params[bq];
-        const uint32_t t = pa.tokens[r];
-        const float Z = S[V - 1];
-        float* slot = pa.out + (size_t)bq * (d1 - 1u) + iq;
-        if (!(Z > 0.0f) || !isfinite(Z) || t >= V) {
-            if (tid == 0) *slot = 0.0f;
-            return;
-        }
-        auto pv = [&](uint32_t j) { return __fdiv_rn(dense[j], Z); };
-        const bool mp_on = pp.has_min_p && isfinite(pp.min_p) && pp.min_p > 0.0f;
-        if (pa.topk == 0 && pp.top_k == 0 && !(pp.top_p < 1.0f) && !mp_on) {
-            if (tid == 0) *slot = pv(t);  // the softmax value itself
-            return;
-        }
-        uint32_t K = V;
-        float tp = pp.top_p;
-        if (pa.topk > 0) K = pa.topk < V ? pa.topk : V;
-        else if (pp.top_k > 0 || pp.top_p < 1.0f) K = (pp.top_k > 0 && pp.top_k < V) ? pp.top_k : V;
-        else tp = 1.0f;
-        const bool cut = isfinite(tp) && tp > 0.0f && tp < 1.0f;
-        const float ptok = pv(t);
-        float lmax = 0.0f;
-        for (uint32_t j = tid; j < V; j += NT_EX) lmax = fmaxf(lmax, pv(j));
-        const float pmax = block_max<NT_EX>(lmax, reinterpret_cast<float*>(s_u));
-        const float cutoff = mp_on ? __fmul_rn(pp.min_p, pmax) : 0.0f;
-        uint32_t cm = 0, cgt = 0, ceq = 0;
-        for (uint32_t j = tid; j < V; j += NT_EX) {
-            const float q = pv(j);
-            cm += (q > 0.0f && q >= cutoff) ? 1u : 0u;
-            cgt += q > ptok ? 1u : 0u;
-            ceq += (q == ptok && j < t) ? 1u : 0u;
-        }
-        const uint32_t n_m = block_sum_u32<NT_EX>(cm, s_u);
-        const uint32_t rank_t = block_sum_u32<NT_EX>(cgt, s_u) + block_sum_u32<NT_EX>(ceq, s_u);
-        const uint32_t Kp = n_m < K ? n_m : K;
-        if (Kp == 0) {
-            if (tid == 0) *slot = 0.0f;
-            return;
-        }
-        // The sorted values in chunks of up to PROD_CAP: the chunk ending at
-        // sorted position `end` is everything above the end-th largest bit
-        // pattern th (p >= 0: bits order as values) plus `want` copies of it,
-        // minus what the previous chunks took (above th0, plus want0 copies
-        // of th0).
-        uint32_t* hist = s_cnt;
-        uint64_t* vk = reinterpret_cast<uint64_t*>(s_cnt + 512);           // PROD_CAP sort keys
-        float* Ss = reinterpret_cast<float*>(s_cnt + 512 + 2 * PROD_CAP);  // running sums
-        auto select = [&](uint32_t rank, uint32_t& th, uint32_t& want) {
-            uint32_t prefix = 0, mask = 0;
-            want = rank;
-            for (int shift = 24; shift >= 0; shift -= 8) {
-                for (uint32_t j = tid; j < 256u; j += NT_EX) hist[j] = 0;
-                __syncthreads();
-                for (uint32_t j = tid; j < V; j += NT_EX) {
-                    const uint32_t bb = __float_as_uint(pv(j));
-                    if ((bb & mask) == prefix && bb != 0u) atomicAdd(&hist[(bb >> shift) & 255u], 1u);
-                }
-                __syncthreads();
-                if (tid == 0) {
-                    uint32_t cum = 0, dg = 0;
-                    for (int q = 255; q >= 0; --q) {
-                        if (cum + hist[q] >= want) {
-                            dg = (uint32_t)q;
-                            break;
-                        }
-                        cum += hist[q];
-                    }
-                    s_k = dg;
-                    s_cross = want - cum;
-                }
-                __syncthreads();
-                prefix |= s_k << shift;
-                mask |= 255u << shift;
-                want = s_cross;
-                __syncthreads();
-            }
-            th = prefix;
-        };
-        uint32_t pos = 0, th0 = 0xFFFFFFFFu, want0 = 0, keep = Kp;
-        float run = 0.0f, fsum = 0.0f;
-        bool found = false;
-        while (pos < Kp) {
-            const uint32_t end = (Kp - pos > PROD_CAP) ? pos + PROD_CAP : Kp;
-            const uint32_t nch = end - pos;
-            uint32_t th, want;
-            select(end, th, want);
-            // copies of th0 left after the previous chunks
-            if (tid == 0) s_k = 0;
+    // Production target law of a draft token (compute_mtp_target_probs,
+    // runner/mod.rs:12025-12159, then extract_cpu_into, :11836-11937, and
+    // filtered_target_token_probability, :11943-12001) over this row's
+    // softmax p_j = q_j / S (full_vocab_token_logprob's terms and
+    // index-order sum).  The filtered laws keep the K largest p
+    // ((p desc, id asc)), those >= min_p * max p, cut where the f32
+    // running sum in that order first reaches top_p, and divide p_t by the
+    // kept sum in that order.  Only values enter the sums, so the sorted
+    // values are walked in chunks of PROD_CAP: each chunk's values found
+    // by a radix select of its last position's value (4 passes of 8 bits
+    // over the row), gathered into LDS, sorted and summed by the exact
+    // block scan from the previous chunk's sum, until the running sum
+    // reaches top_p or the kept prefix ends; t's place in the order is
+    // counted over the row.
+    constexpr uint32_t PROD_CAP = 4096;
+    const uint32_t d1 = (uint32_t)pa.d1, bq = (uint32_t)r / d1, iq = (uint32_t)r % d1;
+    if (iq + 1u >= d1) return;  // the bonus row has no draft position
+    const axs_sampling_params pp = pa.params[bq];
+    const uint32_t t = pa.tokens[r];
+    const float Z = S[V - 1];
+    float* slot = pa.out + (size_t)bq * (d1 - 1u) + iq;
+    if (!(Z > 0.0f) || !isfinite(Z) || t >= V) {
+        if (tid == 0) *slot = 0.0f;
+        return;
+    }
+    auto pv = [&](uint32_t j) { return __fdiv_rn(dense[j], Z); };
+    const bool mp_on = pp.has_min_p && isfinite(pp.min_p) && pp.min_p > 0.0f;
+    if (pa.topk == 0 && pp.top_k == 0 && !(pp.top_p < 1.0f) && !mp_on) {
+        if (tid == 0) *slot = pv(t);  // the softmax value itself
+        return;
+    }
+    uint32_t K = V;
+    float tp = pp.top_p;
+    if (pa.topk > 0) K = pa.topk < V ? pa.topk : V;
+    else if (pp.top_k > 0 || pp.top_p < 1.0f) K = (pp.top_k > 0 && pp.top_k < V) ? pp.top_k : V;
+    else tp = 1.0f;
+    const bool cut = isfinite(tp) && tp > 0.0f && tp < 1.0f;
+    const float ptok = pv(t);
+    float lmax = 0.0f;
+    for (uint32_t j = tid; j < V; j += NT_EX) lmax = fmaxf(lmax, pv(j));
+    const float pmax = block_max<NT_EX>(lmax, reinterpret_cast<float*>(s_u));
+    const float cutoff = mp_on ? __fmul_rn(pp.min_p, pmax) : 0.0f;
+    uint32_t cm = 0, cgt = 0, ceq = 0;
+    for (uint32_t j = tid; j < V; j += NT_EX) {
+        const float q = pv(j);
+        cm += (q > 0.0f && q >= cutoff) ? 1u : 0u;
+        cgt += q > ptok ? 1u : 0u;
+        ceq += (q == ptok && j < t) ? 1u : 0u;
+    }
+    const uint32_t n_m = block_sum_u32<NT_EX>(cm, s_u);
+    const uint32_t rank_t = block_sum_u32<NT_EX>(cgt, s_u) + block_sum_u32<NT_EX>(ceq, s_u);
+    const uint32_t Kp = n_m < K ? n_m : K;
+    if (Kp == 0) {
+        if (tid == 0) *slot = 0.0f;
+        return;
+    }
+    // The sorted values in chunks of up to PROD_CAP: the chunk ending at
+    // sorted position `end` is everything above the end-th largest bit
+    // pattern th (p >= 0: bits order as values) plus `want` copies of it,
+    // minus what the previous chunks took (above th0, plus want0 copies
+    // of th0).
+    uint32_t* hist = s_cnt;
+    uint64_t* vk = reinterpret_cast<uint64_t*>(s_cnt + 512);           // PROD_CAP sort keys
+    float* Ss = reinterpret_cast<float*>(s_cnt + 512 + 2 * PROD_CAP);  // running sums
+    auto select = [&](uint32_t rank, uint32_t& th, uint32_t& want) {
+        uint32_t prefix = 0, mask = 0;
+        want = rank;
+        for (int shift = 24; shift >= 0; shift -= 8) {
+            for (uint32_t j = tid; j < 256u; j += NT_EX) hist[j] = 0;
             __syncthreads();
-            uint32_t ce = 0;
-            for (uint32_t j = tid; j < V; j += NT_EX) ce += __float_as_uint(pv(j)) == th0 ? 1u : 0u;
-            const uint32_t n_th0 = block_sum_u32<NT_EX>(ce, s_u);
-            // strictly between th and th0
             for (uint32_t j = tid; j < V; j += NT_EX) {
                 const uint32_t bb = __float_as_uint(pv(j));
-                if (bb > th && bb < th0) vk[atomicAdd(&s_k, 1u)] = (uint64_t)bb << 32;
+                if ((bb & mask) == prefix && bb != 0u) atomicAdd(&hist[(bb >> shift) & 255u], 1u);
             }
             __syncthreads();
-            uint32_t ng = s_k;
-            const uint32_t c_hi = th < th0 ? (pos > 0 ? n_th0 - want0 : 0u) : 0u;  // th0's remaining copies
-            const uint32_t c_lo = th < th0 ? want : want - want0;                  // copies of th in this chunk
-            const uint32_t np2 = next_pow2(nch);
-            for (uint32_t j = ng + (uint32_t)tid; j < np2; j += NT_EX) {
-                uint64_t kv = 0ull;
-                if (j < ng + c_hi) kv = (uint64_t)th0 << 32;
-                else if (j < ng + c_hi + c_lo) kv = (uint64_t)th << 32;
-                vk[j] = kv;
-            }
-            __threadfence_block();
-            __syncthreads();
-            block_sort_desc<NT_EX>(vk, np2);
-            block_exact_sums<8>([&](uint32_t k) { return __uint_as_float((uint32_t)(vk[k] >> 32)); }, 0u, nch,
-                                 run, Ss, XL.sum);
-            __threadfence_block();
-            __syncthreads();
-            if (cut) {
-                // the first running sum reaching top_p
-                if (tid == 0) s_k = NONE;
-                __syncthreads();
-                uint32_t first = NONE;
-                for (uint32_t k = tid; k < nch; k += NT_EX)
-                    if (Ss[k] >= tp) first = min(first, k);
-                if (first != NONE) atomicMin(&s_k, first);
-                __syncthreads();
-                const uint32_t fk = s_k;
-                __syncthreads();
-                if (fk != NONE) {
-                    keep = pos + fk + 1u;
-                    fsum = Ss[fk];
-                    found = true;
-                    break;
+            if (tid == 0) {
+                uint32_t cum = 0, dg = 0;
+                for (int q = 255; q >= 0; --q) {
+                    if (cum + hist[q] >= want) {
+                        dg = (uint32_t)q;
+                        break;
+                    }
+                    cum += hist[q];
                 }
+                s_k = dg;
+                s_cross = want - cum;
             }
-            run = Ss[nch - 1u];
-            th0 = th;
-            want0 = want;  // copies of th among the first `end` positions
-            pos = end;
+            __syncthreads();
+            prefix |= s_k << shift;
+            mask |= 255u << shift;
+            want = s_cross;
+            __syncthreads();
         }
-        if (!found) fsum = run;  // every kept value summed
-        if (tid == 0)
-            *slot = (ptok > 0.0f && rank_t < keep) ? fmaxf(__fdiv_rn(ptok, fmaxf(fsum, 1e-37f)), 0.0f) : 0.0f;
-        return;
+        th = prefix;
+    };
+    uint32_t pos = 0, th0 = 0xFFFFFFFFu, want0 = 0, keep = Kp;
+    float run = 0.0f, fsum = 0.0f;
+    bool found = false;
+    while (pos < Kp) {
+        const uint32_t end = (Kp - pos > PROD_CAP) ? pos + PROD_CAP : Kp;
+        const uint32_t nch = end - pos;
+        uint32_t th, want;
+        select(end, th, want);
+        // copies of th0 left after the previous chunks
+        if (tid == 0) s_k = 0;
+        __syncthreads();
+        uint32_t ce = 0;
+        for (uint32_t j = tid; j < V; j += NT_EX) ce += __float_as_uint(pv(j)) == th0 ? 1u : 0u;
+        const uint32_t n_th0 = block_sum_u32<NT_EX>(ce, s_u);
+        // strictly between th and th0
+        for (uint32_t j = tid; j < V; j += NT_EX) {
+            const uint32_t bb = __float_as_uint(pv(j));
+            if (bb > th && bb < th0) vk[atomicAdd(&s_k, 1u)] = (uint64_t)bb << 32;
+        }
+        __syncthreads();
+        uint32_t ng = s_k;
+        const uint32_t c_hi = th < th0 ? (pos > 0 ? n_th0 - want0 : 0u) : 0u;  // th0's remaining copies
+        const uint32_t c_lo = th < th0 ? want : want - want0;                  // copies of th in this chunk
+        const uint32_t np2 = next_pow2(nch);
+        for (uint32_t j = ng + (uint32_t)tid; j < np2; j += NT_EX) {
+            uint64_t kv = 0ull;
+            if (j < ng + c_hi) kv = (uint64_t)th0 << 32;
+            else if (j < ng + c_hi + c_lo) kv = (uint64_t)th << 32;
+            vk[j] = kv;
+        }
+        __threadfence_block();
+        __syncthreads();
+        block_sort_desc<NT_EX>(vk, np2);
+        block_exact_sums<8>([&](uint32_t k) { return __uint_as_float((uint32_t)(vk[k] >> 32)); }, 0u, nch,
+                             run, Ss, XL.sum);
+        __threadfence_block();
+        __syncthreads();
+        if (cut) {
+            // the first running sum reaching top_p
+            if (tid == 0) s_k = NONE;
+            __syncthreads();
+            uint32_t first = NONE;
+            for (uint32_t k = tid; k < nch; k += NT_EX)
+                if (Ss[k] >= tp) first = min(first, k);
+            if (first != NONE) atomicMin(&s_k, first);
+            __syncthreads();
+            const uint32_t fk = s_k;
+            __syncthreads();
+            if (fk != NONE) {
+                keep = pos + fk + 1u;
+                fsum = Ss[fk];
+                found = true;
+                break;
+            }
+        }
+        run = Ss[nch - 1u];
+        th0 = th;
+        want0 = want;  // copies of th among the first `end` positions
+        pos = end;
+    }
+    if (!found) fsum = run;  // every kept value summed
+    if (tid == 0)
+        *slot = (ptok > 0.0f && rank_t < keep) ? fmaxf(__fdiv_rn(ptok, fmaxf(fsum, 1e-37f)), 0.0f) : 0.0f;
+    return;
 }
 
 // --------------------------------------------------------------------------
