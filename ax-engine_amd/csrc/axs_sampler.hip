@@ -2715,9 +2715,45 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
     lds_barrier();
     constexpr int XV = 4;  // vectors per thread per tile
     constexpr uint32_t XTILE = (uint32_t)RT * XV * EPV;
+    // The wave's exclusive prefix of per-lane slot bits (n slots per lane)
+    // and its total.  Masked rows: one ballot per slot, and their tiles
+    // double-buffered below (C4: -28 us).  Unmasked rows keep the
+    // cross-lane scan and single tiles: the same changes there move the code
+    // generation of the stream loop the kernel shares with them (C3 +2.5 us,
+    // measured).
+    auto wave_prefix = [&](uint32_t bits, int n, uint32_t& excl, uint32_t& total) {
+        if constexpr (MASK) {
+            excl = 0;
+            total = 0;
+#pragma unroll
+            for (int q = 0; q < EPV; ++q) {
+                if (q >= n) break;
+                const uint64_t bq = __ballot((bits >> q) & 1u);
+                excl += mbcnt64(bq);
+                total += (uint32_t)__popcll(bq);
+            }
+        } else {
+            const uint32_t nc = (uint32_t)__popc(bits);
+            uint32_t incl = nc;
+#pragma unroll
+            for (int d = 1; d < 64; d <<= 1) {
+                const uint32_t y = (uint32_t)__shfl_up((int)incl, d, 64);
+                if (lane >= d) incl += y;
+            }
+            total = (uint32_t)__shfl((int)incl, 63, 64);
+            excl = incl - nc;
+        }
+    };
+    Tile<DT, XV, MASK> Tn;
+    if constexpr (MASK) tile_load<DT, XV, MASK, RT>(a, r, rp, 0u, hi, (uint32_t)tid, Tn);
     for (uint32_t t0 = 0; t0 < hi; t0 += XTILE) {
         Tile<DT, XV, MASK> T;
-        tile_load<DT, XV, MASK, RT>(a, r, rp, t0, hi, (uint32_t)tid, T);
+        if constexpr (MASK) {
+            T = Tn;
+            if (t0 + XTILE < hi) tile_load<DT, XV, MASK, RT>(a, r, rp, t0 + XTILE, hi, (uint32_t)tid, Tn);
+        } else {
+            tile_load<DT, XV, MASK, RT>(a, r, rp, t0, hi, (uint32_t)tid, T);
+        }
 #pragma unroll
         for (int j = 0; j < XV; ++j) {
             const uint32_t e0 = t0 + ((uint32_t)j * RT + (uint32_t)tid) * EPV;
@@ -2738,15 +2774,8 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                     xq[q] = __fmul_rn(__fsub_rn(v[q], xs.m), xs.inv);
                     if (e < hi && xq[q] >= xstage) cm |= 1u << q;
                 }
-                const uint32_t nc = (uint32_t)__popc(cm);
-                uint32_t incl = nc;
-#pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const uint32_t y = (uint32_t)__shfl_up((int)incl, d, 64);
-                    if (lane >= d) incl += y;
-                }
-                const uint32_t tot = (uint32_t)__shfl((int)incl, 63, 64);
-                uint32_t so = incl - nc;
+                uint32_t so, tot;
+                wave_prefix(cm, EPV, so, tot);
 #pragma unroll
                 for (int q = 0; q < EPV; ++q)
                     if ((cm >> q) & 1u) xstg[so++] = ((uint64_t)__float_as_uint(xq[q]) << 32) | (e0 + (uint32_t)q);
@@ -2776,17 +2805,11 @@ __global__ __launch_bounds__(RT) void k_row(KArgs a) {
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
                 // the wave's keys, at one LDS claim per vector
-                const uint32_t mine = (uint32_t)__popc(km);
-                uint32_t kin = mine;
-#pragma unroll
-                for (int d = 1; d < 64; d <<= 1) {
-                    const uint32_t y = (uint32_t)__shfl_up((int)kin, d, 64);
-                    if (lane >= d) kin += y;
-                }
-                const uint32_t ktot = (uint32_t)__shfl((int)kin, 63, 64);
+                uint32_t kex, ktot;
+                wave_prefix(km, EPV, kex, ktot);
                 uint32_t base = 0;
                 if (lane == 0 && ktot) base = atomicAdd(&SL.xn, ktot);
-                uint32_t o = (uint32_t)__shfl((int)base, 0, 64) + kin - mine;
+                uint32_t o = (uint32_t)__shfl((int)base, 0, 64) + kex;
 #pragma unroll
                 for (int i = 0; i < EPV; ++i)
                     if ((km >> i) & 1u) ck[o++] = kk[i];
