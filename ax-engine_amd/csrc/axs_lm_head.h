@@ -29,7 +29,7 @@
 // (argmax_f32, crates/ax-engine-mlx/src/sampling.rs:954-970: larger value
 // wins, ties keep the lower id, NaN never wins, -0 equals +0, an all-NaN row
 // gives 0).  The argmax is carried as a 64-bit key, order-preserving float
-// bits above the complemented id, so a single atomicMax per (workgroup,
+// bits above the complemented id, so at most one atomicMax per (workgroup,
 // batch row) merges workgroups in any order to the same result.  A greedy
 // row therefore gets its token without its logits ever being written or
 // read again.
@@ -108,8 +108,17 @@ __device__ __forceinline__ unsigned long long finish_logit(const LmArgs& a, floa
     return am_key(x, (uint32_t)v);
 }
 
+// Folds a workgroup's best key for one batch row into the global key.  The
+// global key only grows, so a workgroup whose key is not above the value it
+// reads cannot change the result and issues no atomic: every workgroup of a
+// launch targets the same B keys, and unconditional atomics on one address
+// serialise at L2 (at B = 1 they cost more than the weight stream).
+__device__ __forceinline__ void fold_key(unsigned long long* g, unsigned long long k) {
+    if (k > __hip_atomic_load(g, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)) atomicMax(g, k);
+}
+
 // Merges a workgroup's per-wave keys (s_key[wave][j] for batch row b0 + j)
-// into the global keys with one atomicMax per batch row.
+// into the global keys, at most one atomicMax per batch row.
 template <int NW>
 __device__ __forceinline__ void merge_keys(const LmArgs& a, unsigned long long (*s_key)[BMAX], int b0, int nrows) {
     __syncthreads();
@@ -118,34 +127,38 @@ __device__ __forceinline__ void merge_keys(const LmArgs& a, unsigned long long (
         unsigned long long k = s_key[0][t];
 #pragma unroll
         for (int w = 1; w < NW; ++w) k = s_key[w][t] > k ? s_key[w][t] : k;
-        if (k) atomicMax(a.keys + b0 + t, k);
+        fold_key(a.keys + b0 + t, k);
     }
 }
 
 // ---------------------------------------------------------------------------
-// B <= DOT_BMAX: one wave per DOT_ROWS vocabulary rows, each load a 1 KB
-// contiguous piece of one W row (lane l: 8 elements at k0 + 8l), products
-// on the vector ALUs (a bf16 x bf16 product is exact in f32; per lane the
-// H/512 * 8 products of a row accumulate in order, then a 64-lane tree sum).
-// With at most 2 batch rows a matrix-core step would be >= 7/8 padding; the
-// bound is HBM either way, and this load shape reaches more of it.
+// B <= DOT_BMAX: one wave per ROWS vocabulary rows, each load a 1 KB
+// contiguous piece of one W row (lane l: 8 elements at k0 + 8l), DEPTH such
+// pieces per row in flight, products on the vector ALUs (a bf16 x bf16
+// product is exact in f32; per lane the H/512 * 8 products of a row
+// accumulate in K order, then a 64-lane tree sum, so every ROWS x DEPTH
+// shape gives the same bits).  With at most 2 batch rows a matrix-core step
+// would be >= 7/8 padding; the bound is HBM either way, and this load shape
+// reaches more of it.  Measured at H = 4096, V = 151936 on normally
+// distributed weights: the shapes tried (1, 2 or 4 rows x 4, 2 or 1 pieces)
+// lie within 3% of one another; B = 1 is fastest with 2 rows and 2 pieces,
+// B = 2 with 4 rows and 1 piece.
 constexpr int DOT_BMAX = 2;
-constexpr int DOT_ROWS = 4;   // vocabulary rows per wave
 constexpr int DOT_KC = 512;   // K per load (64 lanes x 8 elements)
 
-template <int NBR>
+template <int NBR, int ROWS, int DEPTH>
 __global__ __launch_bounds__(NT) void k_lm_head_dot(LmArgs a) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int vbase = (blockIdx.x * (NT / 64) + wave) * DOT_ROWS;
-    const uint16_t* wrow[DOT_ROWS];
+    const int vbase = (blockIdx.x * (NT / 64) + wave) * ROWS;
+    const uint16_t* wrow[ROWS];
 #pragma unroll
-    for (int r = 0; r < DOT_ROWS; ++r) wrow[r] = a.w + (int64_t)min(vbase + r, a.V - 1) * a.ws + 8 * lane;
+    for (int r = 0; r < ROWS; ++r) wrow[r] = a.w + (int64_t)min(vbase + r, a.V - 1) * a.ws + 8 * lane;
     const uint16_t* hrow[NBR];
 #pragma unroll
     for (int b = 0; b < NBR; ++b) hrow[b] = a.hidden + (int64_t)min(b, a.B - 1) * a.hs + 8 * lane;
-    float acc[DOT_ROWS][NBR];
+    float acc[ROWS][NBR];
 #pragma unroll
-    for (int r = 0; r < DOT_ROWS; ++r)
+    for (int r = 0; r < ROWS; ++r)
 #pragma unroll
         for (int b = 0; b < NBR; ++b) acc[r][b] = 0.0f;
     auto dot8 = [](u32x4 w, u32x4 h, float s) {
@@ -157,31 +170,49 @@ __global__ __launch_bounds__(NT) void k_lm_head_dot(LmArgs a) {
         return s;
     };
     const int hmain = a.H - a.H % DOT_KC;
-    for (int k0 = 0; k0 < hmain; k0 += DOT_KC) {
-        u32x4 wv[DOT_ROWS], hv[NBR];
+    const int hdeep = hmain - hmain % (DOT_KC * DEPTH);
+    int k0 = 0;
+    for (; k0 < hdeep; k0 += DOT_KC * DEPTH) {
+        u32x4 wv[DEPTH][ROWS], hv[DEPTH][NBR];
 #pragma unroll
-        for (int r = 0; r < DOT_ROWS; ++r) wv[r] = *(const u32x4*)(wrow[r] + k0);
+        for (int d = 0; d < DEPTH; ++d) {
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r) wv[d][r] = *(const u32x4*)(wrow[r] + k0 + DOT_KC * d);
+#pragma unroll
+            for (int b = 0; b < NBR; ++b) hv[d][b] = *(const u32x4*)(hrow[b] + k0 + DOT_KC * d);
+        }
+#pragma unroll
+        for (int d = 0; d < DEPTH; ++d)
+#pragma unroll
+            for (int r = 0; r < ROWS; ++r)
+#pragma unroll
+                for (int b = 0; b < NBR; ++b) acc[r][b] = dot8(wv[d][r], hv[d][b], acc[r][b]);
+    }
+    for (; k0 < hmain; k0 += DOT_KC) {  // whole 512-element pieces past the last DEPTH group
+        u32x4 wv[ROWS], hv[NBR];
+#pragma unroll
+        for (int r = 0; r < ROWS; ++r) wv[r] = *(const u32x4*)(wrow[r] + k0);
 #pragma unroll
         for (int b = 0; b < NBR; ++b) hv[b] = *(const u32x4*)(hrow[b] + k0);
 #pragma unroll
-        for (int r = 0; r < DOT_ROWS; ++r)
+        for (int r = 0; r < ROWS; ++r)
 #pragma unroll
             for (int b = 0; b < NBR; ++b) acc[r][b] = dot8(wv[r], hv[b], acc[r][b]);
     }
     if (hmain + 8 * lane < a.H) {  // the last H % 512 (a multiple of 32): lanes below it
-        u32x4 wv[DOT_ROWS], hv[NBR];
+        u32x4 wv[ROWS], hv[NBR];
 #pragma unroll
-        for (int r = 0; r < DOT_ROWS; ++r) wv[r] = *(const u32x4*)(wrow[r] + hmain);
+        for (int r = 0; r < ROWS; ++r) wv[r] = *(const u32x4*)(wrow[r] + hmain);
 #pragma unroll
         for (int b = 0; b < NBR; ++b) hv[b] = *(const u32x4*)(hrow[b] + hmain);
 #pragma unroll
-        for (int r = 0; r < DOT_ROWS; ++r)
+        for (int r = 0; r < ROWS; ++r)
 #pragma unroll
             for (int b = 0; b < NBR; ++b) acc[r][b] = dot8(wv[r], hv[b], acc[r][b]);
     }
     // tree sums: every lane ends with the row totals
 #pragma unroll
-    for (int r = 0; r < DOT_ROWS; ++r)
+    for (int r = 0; r < ROWS; ++r)
 #pragma unroll
         for (int b = 0; b < NBR; ++b)
 #pragma unroll
@@ -190,7 +221,7 @@ __global__ __launch_bounds__(NT) void k_lm_head_dot(LmArgs a) {
     unsigned long long key = 0ull;
     int mine_b = -1;
 #pragma unroll
-    for (int r = 0; r < DOT_ROWS; ++r)
+    for (int r = 0; r < ROWS; ++r)
 #pragma unroll
         for (int b = 0; b < NBR; ++b)
             if (lane == r * NBR + b && b < a.B) {

@@ -5591,11 +5591,14 @@ int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, con
     using namespace axs_lmh;
     timed(ctx, AXS_KERNEL_LM_HEAD, s, [&] {
         if (batch <= DOT_BMAX) {
-            const dim3 grid((unsigned)((vocab + (NT / 64) * DOT_ROWS - 1) / ((NT / 64) * DOT_ROWS)));
+            // B = 1: two vocabulary rows per wave, 2 K pieces of each in
+            // flight; B = 2: four rows per wave, one piece
+            const int rows = batch == 1 ? 2 : 4;
+            const dim3 grid((unsigned)((vocab + (NT / 64) * rows - 1) / ((NT / 64) * rows)));
             if (batch == 1)
-                hipLaunchKernelGGL(k_lm_head_dot<1>, grid, dim3(NT), 0, s, a);
+                hipLaunchKernelGGL((k_lm_head_dot<1, 2, 2>), grid, dim3(NT), 0, s, a);
             else
-                hipLaunchKernelGGL(k_lm_head_dot<2>, grid, dim3(NT), 0, s, a);
+                hipLaunchKernelGGL((k_lm_head_dot<2, 4, 1>), grid, dim3(NT), 0, s, a);
         } else {
             // up to 32 batch rows: 64 vocabulary rows per workgroup, 512-byte
             // K chunks; above: 128 rows per workgroup (each hidden fragment
