@@ -103,9 +103,12 @@ def _argmax_rows(oracle, logits):
     return np.array([oracle.argmax_f32(np.ascontiguousarray(r)) for r in logits], dtype=np.uint32)
 
 
+# B = 1 walks K in groups of two 512-wide pieces, then single pieces, then a
+# tail of H % 512: H = 4096 is whole groups, 2592 a group, one piece and a
+# 32-wide tail, 544 no group; V is odd so the last workgroup's rows pass V.
 @pytest.mark.parametrize("B,H,V,seed", [(1, 4096, 151936, 1), (2, 1056, 7777, 5), (13, 2080, 50021, 2),
                                         (40, 1056, 9001, 6), (64, 4096, 151936, 3), (80, 1024, 32003, 4),
-                                        (200, 512, 20011, 7)])
+                                        (200, 512, 20011, 7), (1, 2592, 30011, 8), (1, 544, 1001, 9)])
 def test_lm_head_matches_exact_product(sampler, oracle, B, H, V, seed):
     import torch
 
