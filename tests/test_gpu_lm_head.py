@@ -125,6 +125,45 @@ def test_lm_head_matches_exact_product(sampler, oracle, B, H, V, seed):
     assert np.array_equal(ids_only.cpu().numpy().view(np.uint32), want)
 
 
+@pytest.mark.parametrize("B", [1, 5])
+def test_lm_head_strided_operands(sampler, oracle, B):
+    """hidden and weight as views into padded buffers (row strides above H,
+    hidden offset by 16 bytes) and an output row stride that is not a
+    multiple of 4 (so no 16-byte stores): the logits are bit-identical to
+    the contiguous call's (the same kernel sums in the same order), within
+    the exact product's bound, and the output's padding columns are not
+    written."""
+    import torch
+
+    from ax_sampler import _abi
+
+    H, V = 1056, 3001
+    log(f"lm_head strided case B={B} H={H} V={V}")
+    hidden, weight = _inputs(B, H, V, 31 + B)
+    hp = torch.zeros((B, H + 40), dtype=torch.bfloat16, device="cuda:0")
+    hp[:, 8:8 + H] = hidden
+    wp = torch.zeros((V, H + 24), dtype=torch.bfloat16, device="cuda:0")
+    wp[:, :H] = weight
+    hv, wv = hp[:, 8:8 + H], wp[:, :H]
+    assert hv.stride(0) == H + 40 and wv.stride(0) == H + 24
+    ref_logits, ref_ids = sampler.lm_head(hidden, weight)
+    os_ = V + 3
+    out = torch.full((B, os_), float("nan"), dtype=torch.float32, device="cuda:0")
+    ids = torch.empty(B, dtype=torch.int32, device="cuda:0")
+    _abi.check(sampler.L.axs_lm_head(sampler.ctx, hv.data_ptr(), hv.stride(0), wv.data_ptr(), wv.stride(0),
+                                     B, H, V, 1.0, 0.0, out.data_ptr(), os_, ids.data_ptr(),
+                                     sampler._stream(None)))
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isnan(got[:, V:]).all()
+    assert np.array_equal(got[:, :V].view(np.uint32), ref_logits.cpu().numpy().view(np.uint32))
+    exact, ab = _exact(hidden, weight)
+    _check_logits(np.ascontiguousarray(got[:, :V]), exact, ab, H, f"strided B={B}")
+    want = _argmax_rows(oracle, np.ascontiguousarray(got[:, :V]))
+    assert np.array_equal(ids.cpu().numpy().view(np.uint32), want)
+    assert np.array_equal(ref_ids.cpu().numpy().view(np.uint32), want)
+
+
 def test_lm_head_scale_and_softcap(sampler, oracle):
     import torch
 
