@@ -54,10 +54,12 @@ WORKLOADS = {
           "top_p 0.95, min_p 0.02, 2048-token histories, Philox draws",
     "C4": "C4: B=128 V=151936 f32, allowed-token bitmask 5-60%, 32 bias entries/row, T 1.0, top_p 0.9",
     "C5": "C5: MTP verify B=32 depth 3 V=151936 bf16, target [B,4,V] + draft [B,3,V], T 0.6, top_p 0.95",
+    "F1": "F1: LM head + greedy argmax (producer fusion) B=1 H=4096 V=151936, bf16 hidden and weight, "
+          "token id only (logits not written)",
     "F2": "F2: LM head + greedy argmax (producer fusion) B=64 H=4096 V=151936, bf16 hidden and weight, "
           "f32 logits written",
 }
-F2_SHAPE = (64, 4096, 151936)  # batch rows, hidden size, vocabulary
+LM_HEAD_SHAPES = {"F1": (1, 4096, 151936), "F2": (64, 4096, 151936)}  # batch rows, hidden size, vocabulary
 
 
 def log(msg):
@@ -232,12 +234,13 @@ def main():
     stream = torch.cuda.current_stream(dev)
     s = HipSampler(0, max_batch=256, max_vocab=262144)
     t0 = time.perf_counter()
-    if cfg == "F2":
-        B, H, V = F2_SHAPE
+    if cfg in LM_HEAD_SHAPES:
+        B, H, V = LM_HEAD_SHAPES[cfg]
         gen = torch.Generator(device=dev).manual_seed(2)
         weight = (torch.randn(V, H, device=dev, generator=gen) * 0.02).to(torch.bfloat16)
         hidden = torch.randn(B, H, device=dev, generator=gen).to(torch.bfloat16)
-        logits = torch.empty((B, V), dtype=torch.float32, device=dev)
+        # F1 is a greedy decode step: only the token id leaves the kernel
+        logits = torch.empty((B, V), dtype=torch.float32, device=dev) if cfg == "F2" else None
         ids = torch.empty(B, dtype=torch.int32, device=dev)
         log(f"workload generated in {time.perf_counter() - t0:.1f}s")
         sptr = s._stream(stream)
@@ -247,12 +250,13 @@ def main():
 
         def step(i):
             _abi.check(s.L.axs_lm_head(s.ctx, hidden.data_ptr(), H, weight.data_ptr(), H, B, H, V, 1.0, 0.0,
-                                       logits.data_ptr(), V, ids.data_ptr(), sptr))
+                                       logits.data_ptr() if logits is not None else None,
+                                       V if logits is not None else 0, ids.data_ptr(), sptr))
             return _Res
 
         rows_per_step = B
         # the weight (1.24 GB, larger than the MALL) is read once per step
-        alg = V * H * 2 + B * H * 2 + B * V * 4 + B * 4
+        alg = V * H * 2 + B * H * 2 + (B * V * 4 if logits is not None else 0) + B * 4
         unit_rows = "rows/s"
     elif cfg == "C5":
         from oracle import oracle
@@ -336,7 +340,7 @@ def main():
         dom_alg = alg
     elif dom_name == "k_exact_mat":
         # the second pass re-reads the listed rows (and their mask words)
-        fl = res.flags.cpu().numpy().view(np.uint32) if cfg not in ("C5", "F2") else None
+        fl = res.flags.cpu().numpy().view(np.uint32) if cfg not in ("C5", "F1", "F2") else None
         n_ex = int(np.count_nonzero(fl & np.uint32(_abi.FLAG_EXACT_PATH))) if fl is not None else rows_per_step
         dom_alg = int(alg * n_ex / max(rows_per_step, 1))
     else:
@@ -345,7 +349,7 @@ def main():
 
     cpu = None
     if not args.no_cpu_baseline:
-        if cfg == "F2":
+        if cfg in LM_HEAD_SHAPES:
             cb, sample = cpu_baseline_lm_head(torch, hidden, weight)
         elif cfg == "C5":
             cb, sample = cpu_baseline_mtp(t, d, tp, dp, dids)
@@ -374,7 +378,7 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "f32" if cfg in ("C1", "C4") else "bf16",
-        "data": ("synthetic (seeded; the 1.24 GB weight exceeds the 256 MB MALL)" if cfg == "F2"
+        "data": ("synthetic (seeded; the 1.24 GB weight exceeds the 256 MB MALL)" if cfg in LM_HEAD_SHAPES
                  else "synthetic (seeded, rotating input sets over more than 512 MB)"),
         "config": {"workload": WORKLOADS[cfg], "global_batch": rows_per_step},
         "roofline": {
