@@ -85,8 +85,9 @@ def profile_figures(cfg):
     return out
 
 
-def cpu_rows_per_s(fn, rows_per_call, seconds=12.0, max_threads=16):
-    """Times fn(nthreads) on 1 thread and on the host's cores (at most 16)."""
+def cpu_rows_per_s(fn, rows_per_call, seconds=12.0, max_threads=16, max_calls=64):
+    """Times fn(nthreads) on 1 thread and on the host's cores (at most 16):
+    each for seconds / 2 or max_calls calls, whichever ends first."""
     res = {}
     for threads in (1, min(max_threads, os.cpu_count() or 1)):
         n, t0 = 0, time.perf_counter()
@@ -94,7 +95,7 @@ def cpu_rows_per_s(fn, rows_per_call, seconds=12.0, max_threads=16):
             fn(threads)
             n += rows_per_call
             el = time.perf_counter() - t0
-            if el >= seconds / 2 or n >= 64 * rows_per_call:
+            if el >= seconds / 2 or n >= max_calls * rows_per_call:
                 break
         res[threads] = (n / el, n, el)
     return res
@@ -151,7 +152,7 @@ def cpu_baseline_lm_head(torch, hidden, weight):
         y = (h @ w.T).to(torch.bfloat16).float()
         y.argmax(dim=1)
 
-    res = cpu_rows_per_s(fn, B)
+    res = cpu_rows_per_s(fn, B, max_calls=1 << 20)  # time-bounded: 6 s per thread count
     scale = part / V  # rows/s over the slice -> over the full vocabulary
     res = {k: (v[0] * scale, v[1], v[2]) for k, v in res.items()}
     return res, (f"all {B} batch rows against {part} of the {V} weight rows (f32 matmul of the bf16 values, "
