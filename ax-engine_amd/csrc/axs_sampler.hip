@@ -5603,10 +5603,10 @@ int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, con
             // up to 48 batch rows: 64 vocabulary rows per workgroup, 512-byte
             // K chunks; above: 128 rows per workgroup (each hidden fragment
             // feeds two matrix-core steps), 256-byte chunks.  A launch slice
-            // covers 16 * nb batch rows (nb 1-4, or 8 above 64 rows), so W
-            // is read once per 128 batch rows.
+            // covers 16 * nb batch rows (nb 1-4; 6 for 65-96 rows, 8 above),
+            // so W is read once per 128 batch rows.
             const int need = batch < BMAX ? (batch + 15) / 16 : BMAX / 16;  // 16-row batch blocks
-            const int nb = need <= 4 ? need : 8;
+            const int nb = need <= 4 ? need : (need <= 6 ? 6 : 8);
             const int rows = nb <= 3 ? 64 : 128;
             const dim3 grid((unsigned)((vocab + rows - 1) / rows), (unsigned)((batch + 16 * nb - 1) / (16 * nb)));
             switch (nb) {
@@ -5614,6 +5614,7 @@ int axs_lm_head(axs_context* ctx, const void* hidden, int64_t hidden_stride, con
                 case 2: hipLaunchKernelGGL((k_lm_head_mfma<2, 1, 256>), grid, dim3(NT), 0, s, a); break;
                 case 3: hipLaunchKernelGGL((k_lm_head_mfma<3, 1, 256>), grid, dim3(NT), 0, s, a); break;
                 case 4: hipLaunchKernelGGL((k_lm_head_mfma<4, 2, 128>), grid, dim3(NT), 0, s, a); break;
+                case 6: hipLaunchKernelGGL((k_lm_head_mfma<6, 2, 128>), grid, dim3(NT), 0, s, a); break;
                 default: hipLaunchKernelGGL((k_lm_head_mfma<8, 2, 128>), grid, dim3(NT), 0, s, a); break;
             }
         }
